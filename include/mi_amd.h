@@ -1,0 +1,211 @@
+/*
+ * mi_amd.h -- C ABI of the MI355X (gfx950) ragged paged-attention library.
+ *
+ * Every entry point is `extern "C"`, takes raw device pointers, element
+ * strides and sizes, and a HIP stream passed as `void*` (a hipStream_t; NULL
+ * is the legacy default stream).  Calls are asynchronous on that stream: no
+ * entry point synchronises the device, reads device memory on the host or
+ * allocates memory.  Entry points return MI_OK (0) or a negative MI_ERR_*
+ * code; mi_last_error() then returns a message for the calling thread.
+ *
+ * KV-pool layout ("NHD", one pool per layer):
+ *   pool[num_pages][2][page_size][num_kv_heads][head_dim] bf16, contiguous,
+ *   K at index 0 and V at index 1 of the second axis
+ *   (reference: scheduler.py:168-202, PagedKVCache.kv_data).
+ *
+ * Page table in CSR form, int32 device arrays
+ *   (reference: scheduler.py:267-302, build_csr_metadata):
+ *   kv_indptr[batch+1], kv_indices[kv_indptr[batch]], kv_last_page_len[batch];
+ *   request b owns pages kv_indices[kv_indptr[b] .. kv_indptr[b+1]) and holds
+ *   kv_len_b = (npages_b - 1) * page_size + kv_last_page_len[b] tokens
+ *   (0 when npages_b == 0).
+ */
+#ifndef MI_AMD_H_
+#define MI_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* mi_stream_t; /* a hipStream_t */
+
+#define MI_OK 0
+#define MI_ERR_INVALID (-1)     /* bad argument: shape, size, alignment, range  */
+#define MI_ERR_UNSUPPORTED (-2) /* head_dim / group size / page size not built  */
+#define MI_ERR_WORKSPACE (-3)   /* caller-supplied workspace too small          */
+#define MI_ERR_LAUNCH (-4)      /* HIP runtime reported an error on launch      */
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* mi_last_error(void);
+
+/* Library ABI version (major * 10000 + minor * 100 + patch). */
+int mi_version(void);
+
+/* ------------------------------------------------------------------------ *
+ * Paged KV append.
+ * Replaces flashinfer.page.append_paged_kv_cache as called at
+ * model.py:207-216 (positional: append_key, append_value, batch_indices,
+ * positions, paged_kv_cache, kv_indices, kv_indptr, kv_last_page_len).
+ *
+ * For token i: b = batch_indices[i], p = positions[i]; K row i (all heads) is
+ * written to pool[kv_indices[kv_indptr[b] + p / page_size]][0][p % page_size]
+ * and the V row to [..][1][..].  A token whose page slot lies outside request
+ * b's page list (kv_indptr[b] + p/page_size >= kv_indptr[b+1]), or whose page
+ * id is outside [0, num_pages), is not written.
+ * key/value: [num_tokens][num_kv_heads][head_dim] bf16 with the given element
+ * strides (head_dim contiguous; rows 16-byte aligned).
+ * ------------------------------------------------------------------------ */
+int mi_paged_kv_append(const void* append_key, int64_t key_stride_token, int64_t key_stride_head,
+                       const void* append_value, int64_t value_stride_token,
+                       int64_t value_stride_head, const int32_t* batch_indices,
+                       const int32_t* positions, int64_t num_tokens, void* paged_kv_cache,
+                       int64_t num_pages, const int32_t* kv_indices, const int32_t* kv_indptr,
+                       const int32_t* kv_last_page_len, int32_t batch_size, int32_t num_kv_heads,
+                       int32_t head_dim, int32_t page_size, mi_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Split-K paged decode attention.
+ * Replaces flashinfer.decode.BatchDecodeWithPagedKVCacheWrapper:
+ *   plan  -- scheduler.py:402-413, 905-916, 927-938
+ *   run   -- model.py:235 (mode == "decode")
+ *
+ * mi_decode_plan runs a one-workgroup GPU kernel that reads kv_indptr and
+ * kv_last_page_len and writes the split-K work list into `workspace`; it does
+ * not touch the host.  mi_decode_run reads only the work list, so one plan
+ * serves every layer of a step and a graph-captured run replays correctly
+ * after any later plan with the same (batch_size, heads, head_dim) shape.
+ *
+ * q / out: [batch][num_qo_heads][head_dim] bf16 (element strides given).
+ * Q head h reads KV head h / (num_qo_heads / num_kv_heads): any integer group
+ * size 1..8 runs natively (no head padding).  sm_scale <= 0 selects
+ * 1/sqrt(head_dim).  head_dim in {64, 128, 256}; page_size == 16.
+ * ------------------------------------------------------------------------ */
+size_t mi_decode_workspace_size(int32_t batch_size, int32_t num_qo_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int32_t max_units);
+
+int mi_decode_plan(void* workspace, size_t workspace_bytes, const int32_t* kv_indptr,
+                   const int32_t* kv_last_page_len, int32_t batch_size, int32_t num_qo_heads,
+                   int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int32_t max_units,
+                   mi_stream_t stream);
+
+int mi_decode_run(void* workspace, size_t workspace_bytes, const void* q, int64_t q_stride_batch,
+                  int64_t q_stride_head, const void* paged_kv_cache, int64_t num_pages,
+                  const int32_t* kv_indices, void* out, int64_t out_stride_batch,
+                  int64_t out_stride_head, int32_t batch_size, int32_t num_qo_heads,
+                  int32_t num_kv_heads, int32_t head_dim, int32_t page_size, float sm_scale,
+                  int32_t max_units, mi_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Ragged (varlen) paged prefill attention on bf16 MFMA.
+ * Replaces flashinfer.prefill.BatchPrefillWithPagedKVCacheWrapper:
+ *   plan  -- scheduler.py:704-716 (qo_indptr, paged_kv_indptr,
+ *            paged_kv_indices, paged_kv_last_page_len, causal=True)
+ *   run   -- model.py:235 (mode == "prefill")
+ *
+ * q / out: [total_q][num_qo_heads][head_dim] bf16, rows of request b are
+ * qo_indptr[b] .. qo_indptr[b+1].  With causal != 0, query row i of request b
+ * attends to KV tokens j <= i + (kv_len_b - qo_len_b) (bottom-right aligned).
+ * total_q must be >= qo_indptr[batch_size]; it sizes the launch on the host.
+ * head_dim in {64, 128}; page_size == 16.
+ * ------------------------------------------------------------------------ */
+size_t mi_prefill_workspace_size(int32_t batch_size, int64_t total_q);
+
+int mi_prefill_plan(void* workspace, size_t workspace_bytes, const int32_t* qo_indptr,
+                    const int32_t* kv_indptr, const int32_t* kv_last_page_len, int32_t batch_size,
+                    int64_t total_q, int32_t page_size, mi_stream_t stream);
+
+int mi_prefill_run(void* workspace, size_t workspace_bytes, const void* q, int64_t q_stride_token,
+                   int64_t q_stride_head, const void* paged_kv_cache, int64_t num_pages,
+                   const int32_t* kv_indices, void* out, int64_t out_stride_token,
+                   int64_t out_stride_head, int32_t batch_size, int64_t total_q,
+                   int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                   int32_t page_size, int32_t causal, float sm_scale, mi_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Fused batched sampler.
+ * Replaces sample_batch (scheduler.py:319-343) and sample (310-316).
+ *
+ * logits: [batch][vocab] bf16 rows (row stride in elements).
+ * temperature[b] (float, device) is rounded to bf16 as the reference does
+ * (its temperature tensor has the logits dtype).  Rows with temperature <= 0
+ * take argmax(logits) (lowest index among equal maxima; NaN ranks highest).
+ * Other rows draw from softmax(bf16(logit / temperature)) in fp32, restricted
+ * to the top-p nucleus when top_p != NULL and top_p[b] < 1 (the smallest set
+ * of highest-probability tokens whose mass reaches top_p; tokens tied with the
+ * smallest kept probability are kept).  Draws use Philox4x32-10 keyed by
+ * `seed`, with the 64-bit counter *rng_offset (device) advanced once per call
+ * on the stream, so graph replays draw fresh numbers.
+ * out_tokens: [batch] int64 device.
+ * ------------------------------------------------------------------------ */
+int mi_sample(const void* logits, int64_t logits_row_stride, int32_t batch_size, int32_t vocab_size,
+              const float* temperature, const float* top_p, uint64_t seed, uint64_t* rng_offset,
+              int64_t* out_tokens, mi_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Device page table: FIFO free-page ring + per-slot page lists, and the CSR
+ * metadata build for a decode step.
+ * Replaces PagedKVCache.allocate_pages / release_pages
+ * (scheduler.py:208-221), the admission / growth / retire allocator call
+ * order (scheduler.py:624-637, 843-847, 984-1003), build_csr_metadata
+ * (scheduler.py:267-302) and the decode metadata + graph padding
+ * (scheduler.py:862-901).
+ *
+ * State lives in one caller-owned int32 device buffer of
+ * mi_page_table_state_size() bytes.  Pages 0 .. num_pages-2 start on the free
+ * ring in ascending order; page num_pages-1 is the scratch page.
+ *
+ * mi_page_table_step applies, in this order (the reference's deque order):
+ *   1. release: the pages of each slot in release_slots[0..n_release), in
+ *      order, are appended to the ring tail and the slot emptied;
+ *   2. admit: slot admit_slots[k] receives admit_npages[k] pages popped from
+ *      the ring head, k ascending;
+ *   3. grow: for each decode row i in order, slot decode_slots[i] receives
+ *      pages until it holds ceil((decode_pos[i] + 1) / page_size);
+ *   4. CSR: for rows i < n_decode, indptr/indices/last_page_len for
+ *      seq_len = decode_pos[i] + 1, batch_indices[i] = i,
+ *      positions[i] = decode_pos[i]; rows n_decode .. padded_batch-1 are
+ *      graph padding and own exactly the scratch page with last_page_len 1
+ *      and position 0, so their appends land in the scratch page.
+ * `ops` is a device int32 array laid out as
+ *   [n_release][n_admit][n_decode][padded_batch]
+ *   release_slots[n_release] admit_slots[n_admit] admit_npages[n_admit]
+ *   decode_slots[n_decode] decode_pos[n_decode]
+ * Outputs (device int32): indptr[padded_batch+1], indices[capacity],
+ * last_page_len[padded_batch], batch_indices[padded_batch],
+ * positions[padded_batch].  Released page ids are written, in release order,
+ * to released_pages (device int32, may be NULL) for mi_pages_zero.  A pop from
+ * an empty ring, a slot overflow or an indices overflow sets the sticky error
+ * word read by mi_page_table_error_word (device int32 at the returned offset);
+ * the host mirrors free counts and never lets that happen.
+ * ------------------------------------------------------------------------ */
+size_t mi_page_table_state_size(int32_t num_pages, int32_t max_slots, int32_t max_pages_per_slot);
+
+int mi_page_table_init(void* state, int32_t num_pages, int32_t max_slots,
+                       int32_t max_pages_per_slot, mi_stream_t stream);
+
+int mi_page_table_step(void* state, int32_t num_pages, int32_t max_slots,
+                       int32_t max_pages_per_slot, const int32_t* ops, int32_t ops_len,
+                       int32_t page_size, int32_t* indptr, int32_t* indices,
+                       int64_t indices_capacity, int32_t* last_page_len, int32_t* batch_indices,
+                       int32_t* positions, int32_t* released_pages, mi_stream_t stream);
+
+/* Byte offset of the sticky error word inside the state buffer. */
+size_t mi_page_table_error_offset(int32_t num_pages, int32_t max_slots,
+                                  int32_t max_pages_per_slot);
+
+/* Zero `n_pages` pages (ids in page_ids, device int32) in each of `num_layers`
+ * pools laid out back to back with `layer_stride_bytes` between pools; each
+ * page is `page_bytes` long.  Reference: release_pages zeroes each page of
+ * each layer (scheduler.py:216-221). */
+int mi_pages_zero(void* pools, int64_t layer_stride_bytes, int32_t num_layers,
+                  int64_t num_pages, int64_t page_bytes, const int32_t* page_ids, int32_t n_pages,
+                  mi_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI_AMD_H_ */

@@ -1,0 +1,114 @@
+// Shared device helpers and host error plumbing for the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mi_amd.h"
+
+namespace mi {
+
+// ---------------------------------------------------------------- host side
+// Records a printf-style message as the calling thread's last error and
+// returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clears the calling thread's last error.
+void clear_error();
+// Converts a pending HIP launch error into MI_ERR_LAUNCH.
+int check_launch(const char* what);
+// Number of compute units of the current device (cached per device).
+int num_cus();
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// ---------------------------------------------------------------- bf16
+// bf16 bits <-> fp32.  Rounding is to nearest even; NaN maps to a quiet NaN
+// with the sign kept, which is what torch's float->bfloat16 cast produces.
+__device__ __forceinline__ float bf16_lo(uint32_t packed) { return __uint_as_float(packed << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t packed) {
+  return __uint_as_float(packed & 0xffff0000u);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+}
+
+// ---------------------------------------------------------------- MFMA types
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// D(16x16 fp32) += A(16x32 bf16) * B(32x16 bf16).  Lane l supplies A row
+// (l & 15), B column (l & 15), both at k = 8 * (l >> 4) + [0, 8); lane l
+// receives D rows 4 * (l >> 4) + [0, 4) of column (l & 15).
+__device__ __forceinline__ f32x4_t mfma_16x16x32_bf16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------- cross-lane
+// DPP controls (gfx9 encoding).
+constexpr int kDppQuadSwap1 = 0xB1;    // quad_perm [1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4E;    // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+// Max / sum over each aligned group of 16 lanes; every lane gets the result.
+__device__ __forceinline__ float group16_max(float x) {
+  x = fmaxf(x, dpp<kDppQuadSwap1>(x));
+  x = fmaxf(x, dpp<kDppQuadSwap2>(x));
+  x = fmaxf(x, dpp<kDppRowHalfMirror>(x));
+  x = fmaxf(x, dpp<kDppRowMirror>(x));
+  return x;
+}
+__device__ __forceinline__ float group16_sum(float x) {
+  x += dpp<kDppQuadSwap1>(x);
+  x += dpp<kDppQuadSwap2>(x);
+  x += dpp<kDppRowHalfMirror>(x);
+  x += dpp<kDppRowMirror>(x);
+  return x;
+}
+
+// Value of `x` held by lane `src` (0..63), for every lane.
+__device__ __forceinline__ float lane_shuffle(float x, int src) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(x)));
+}
+__device__ __forceinline__ int lane_shuffle_i(int x, int src) {
+  return __builtin_amdgcn_ds_bpermute(src << 2, x);
+}
+// Wave-uniform value of `x` in lane `src` (src must be uniform).
+__device__ __forceinline__ float read_lane(float x, int src) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), src));
+}
+__device__ __forceinline__ int read_lane_i(int x, int src) { return __builtin_amdgcn_readlane(x, src); }
+
+__device__ __forceinline__ float wave_max(float x) {
+  x = group16_max(x);
+  x = fmaxf(x, lane_shuffle(x, (threadIdx.x & 63) ^ 16));
+  x = fmaxf(x, lane_shuffle(x, (threadIdx.x & 63) ^ 32));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  x = group16_sum(x);
+  x += lane_shuffle(x, (threadIdx.x & 63) ^ 16);
+  x += lane_shuffle(x, (threadIdx.x & 63) ^ 32);
+  return x;
+}
+
+__device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ void store16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+}  // namespace mi

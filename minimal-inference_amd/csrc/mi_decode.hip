@@ -1,0 +1,609 @@
+// Split-K paged decode attention for gfx950.
+//
+// Reference: the decode wrapper's plan() (scheduler.py:402-413, 905-916,
+// 927-938) and run() (model.py:235); the math is softmax(q K^T * scale) V over
+// the request's kv_len tokens with KV head h / group for Q head h
+// (model.py:286-295 restates it with repeat_interleave + SDPA).
+//
+// Work decomposition.  plan() cuts every request's page list into `nsplit`
+// contiguous page ranges ("items") so that items x kv_heads ("units") is close
+// to 8 units per CU.  One 64-lane wave runs one unit: it streams the unit's K
+// and V pages for one KV head and serves all `group` Q heads of that KV head,
+// so each KV byte is read from HBM once per step.
+//
+// Per 16-token page, one wave:
+//   * S = Q K^T with four 16x16x32 bf16 MFMAs (head_dim 128): Q rows are the
+//     group's heads (zero-padded to 16), K columns are the page's tokens, and
+//     each lane's 16-byte global load of K is directly its B operand;
+//   * online softmax in the exp2 domain with a lazy running max (rescale only
+//     when the max grows by more than 2^8, so rescales are rare);
+//   * O += P V on the VALU: lane (t, c) holds 8..32 head_dim values of token t
+//     and accumulates them for all group heads; P reaches it by ds_bpermute.
+// At the end the per-token partial sums are reduced through LDS.  Units of a
+// request with several splits write (O, m, l) partials; the last unit to
+// finish (device-scope counter) merges them and resets the counter, so run()
+// is a single launch and needs no memset.
+#include <math.h>
+
+#include "mi_common.h"
+
+namespace {
+
+constexpr int kPageSize = 16;
+constexpr float kLazyRescale = 8.0f;  // log2 units
+constexpr int kMaxSplits = 64;        // splits per request (one lane each in the merge)
+constexpr int kUnitsPerCU = 8;
+
+struct alignas(32) DecodeItem {
+  int b;           // request
+  int page_begin;  // absolute position in kv_indices
+  int page_end;
+  int last_valid;  // valid tokens in the item's final page (0 when empty)
+  int split;
+  int nsplit;
+  int item_base;  // item index of split 0 of this request
+  int pad;
+};
+
+struct DecodeHeader {
+  int num_units;
+  int num_items;
+  int chunk_pages;
+  int error;
+};
+
+struct DecodeLayout {
+  size_t items, counters, pml, po, total;
+  int max_items;
+};
+
+DecodeLayout decode_layout(int batch, int hq, int hkv, int head_dim, int max_units) {
+  const int group = hq / hkv;
+  DecodeLayout L;
+  L.max_items = max_units / hkv;
+  size_t off = 256;  // header
+  L.items = off;
+  off = mi::align_up(off + size_t(L.max_items) * sizeof(DecodeItem), 256);
+  L.counters = off;
+  off = mi::align_up(off + size_t(batch) * hkv * sizeof(int), 256);
+  L.pml = off;
+  off = mi::align_up(off + size_t(max_units) * group * 2 * sizeof(float), 256);
+  L.po = off;
+  off = mi::align_up(off + size_t(max_units) * group * head_dim * sizeof(float), 256);
+  L.total = off;
+  return L;
+}
+
+int default_max_units(int batch, int hkv) {
+  return 2 * mi::num_cus() * kUnitsPerCU + batch * hkv;
+}
+
+// ------------------------------------------------------------------ plan
+struct PlanParams {
+  const int32_t* indptr;
+  const int32_t* last_page_len;
+  int batch, hkv, target_units, max_items;
+  DecodeHeader* header;
+  DecodeItem* items;
+  int* counters;
+};
+
+__device__ int block_sum(int v, int* scratch) {
+  // Wave sums by xor-shuffle, then the per-wave partials through LDS.
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  __syncthreads();
+  if (lane == 0) scratch[w] = v;
+  __syncthreads();
+  int s = 0;
+  for (int i = 0; i < int(blockDim.x >> 6); ++i) s += scratch[i];
+  __syncthreads();
+  return s;
+}
+
+__device__ int block_max(int v, int* scratch) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
+  __syncthreads();
+  if (lane == 0) scratch[w] = v;
+  __syncthreads();
+  int s = scratch[0];
+  for (int i = 1; i < int(blockDim.x >> 6); ++i) s = max(s, scratch[i]);
+  __syncthreads();
+  return s;
+}
+
+// Inclusive scan over the block (Hillis-Steele in LDS); *total receives the
+// block-wide sum.  Ends with a barrier, so `buf` may be reused at once.
+__device__ int block_inclusive_scan(int v, int* buf, int* total) {
+  const int t = threadIdx.x;
+  buf[t] = v;
+  __syncthreads();
+  for (int o = 1; o < int(blockDim.x); o <<= 1) {
+    int add = (t >= o) ? buf[t - o] : 0;
+    __syncthreads();
+    buf[t] += add;
+    __syncthreads();
+  }
+  const int r = buf[t];
+  *total = buf[blockDim.x - 1];
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
+  __shared__ int red[16];
+  __shared__ int scan[1024];
+  const int t = threadIdx.x;
+  int tot = 0, mx = 0;
+  for (int b = t; b < p.batch; b += blockDim.x) {
+    const int np = max(0, p.indptr[b + 1] - p.indptr[b]);
+    tot += np;
+    mx = max(mx, np);
+  }
+  const int total_pages = block_sum(tot, red);
+  const int max_np = block_max(mx, red);
+  // Pages per item: aim at target_units units, never more than kMaxSplits
+  // splits per request, never more items than the workspace holds.
+  long long want = (long long)total_pages * p.hkv;
+  int chunk = int((want + p.target_units - 1) / p.target_units);
+  chunk = max(chunk, 1);
+  chunk = max(chunk, (max_np + kMaxSplits - 1) / kMaxSplits);
+  for (;;) {
+    int cnt = 0;
+    for (int b = t; b < p.batch; b += blockDim.x) {
+      const int np = max(0, p.indptr[b + 1] - p.indptr[b]);
+      cnt += max(1, (np + chunk - 1) / chunk);
+    }
+    const int items = block_sum(cnt, red);
+    if (items <= p.max_items || chunk >= max_np) break;
+    chunk *= 2;
+  }
+  int running = 0;
+  for (int base = 0; base < p.batch; base += blockDim.x) {
+    const int b = base + t;
+    int np = 0, ns = 0;
+    if (b < p.batch) {
+      np = max(0, p.indptr[b + 1] - p.indptr[b]);
+      ns = max(1, (np + chunk - 1) / chunk);
+    }
+    int chunk_total = 0;
+    const int incl = block_inclusive_scan(ns, scan, &chunk_total);
+    const int first = running + incl - ns;
+    if (b < p.batch && first + ns <= p.max_items) {
+      int lpl = p.last_page_len[b];
+      lpl = min(max(lpl, 1), kPageSize);
+      const int pb0 = p.indptr[b];
+      for (int s = 0; s < ns; ++s) {
+        DecodeItem it;
+        it.b = b;
+        it.page_begin = pb0 + int((long long)s * np / ns);
+        it.page_end = pb0 + int((long long)(s + 1) * np / ns);
+        it.last_valid = (np == 0) ? 0 : (s == ns - 1 ? lpl : kPageSize);
+        it.split = s;
+        it.nsplit = ns;
+        it.item_base = first;
+        it.pad = 0;
+        p.items[first + s] = it;
+      }
+    }
+    running += chunk_total;
+  }
+  for (int i = t; i < p.batch * p.hkv; i += blockDim.x) p.counters[i] = 0;
+  if (t == 0) {
+    const int items = min(running, p.max_items);
+    p.header->num_items = items;
+    p.header->num_units = items * p.hkv;
+    p.header->chunk_pages = chunk;
+    p.header->error = (running > p.max_items) ? 1 : 0;
+  }
+}
+
+// ------------------------------------------------------------------ run
+template <int D, int G>
+struct DecodeTraits {
+  static constexpr int KSTEPS = D / 32;                       // MFMA k-steps for q.k
+  static constexpr int DL = (G <= 4 && D >= 128) ? 32 : 16;  // head_dim values per lane in P.V
+  static constexpr int LPT = D / DL;                          // lanes per token row
+  static constexpr int TPP = 64 / LPT;                        // tokens per pass
+  static constexpr int PASSES = kPageSize / TPP;
+  static constexpr int VL = DL / 8;   // 16-byte V loads per pass
+  static constexpr int OUT = D / 64;  // reduced outputs per head per lane
+  static_assert(TPP <= kPageSize && kPageSize % TPP == 0, "pass geometry");
+  static_assert(G >= 1 && G <= 8, "group size");
+};
+
+struct RunParams {
+  const DecodeHeader* header;
+  const DecodeItem* items;
+  int* counters;
+  float* pml;
+  float* po;
+  const uint16_t* q;
+  int64_t q_sb, q_sh;
+  const uint16_t* pool;
+  int64_t num_pages;
+  const int32_t* indices;
+  uint16_t* out;
+  int64_t o_sb, o_sh;
+  int hkv;
+  float scale_log2;
+};
+
+template <int D, int G>
+__device__ __forceinline__ void decode_unit(const RunParams& p, int u, float (*red)[D + 4]) {
+  using T = DecodeTraits<D, G>;
+  const int lane = threadIdx.x;
+  const int item_idx = u / p.hkv;
+  const int hkv = u - item_idx * p.hkv;
+  const DecodeItem it = p.items[item_idx];
+  const int b = it.b;
+
+  const int64_t tok_stride = int64_t(p.hkv) * D;
+  const int64_t kv_stride = kPageSize * tok_stride;
+  const int64_t page_stride = 2 * kv_stride;
+
+  // Q as the A operand: row m = head within the group.
+  const int m = lane & 15, kb = lane >> 4;
+  mi::bf16x8_t qa[T::KSTEPS];
+  {
+    const uint16_t* qrow = p.q + int64_t(b) * p.q_sb + int64_t(hkv * G + (m < G ? m : 0)) * p.q_sh + kb * 8;
+#pragma unroll
+    for (int s = 0; s < T::KSTEPS; ++s) {
+      uint4 v = mi::load16(qrow + s * 32);
+      if (m >= G) v = make_uint4(0, 0, 0, 0);
+      qa[s] = mi::as_bf16x8(v);
+    }
+  }
+  const int tv = lane % T::TPP, cv = lane / T::TPP;
+  const int64_t k_off = int64_t(m) * tok_stride + int64_t(hkv) * D + kb * 8;
+  const int64_t v_off = kv_stride + int64_t(tv) * tok_stride + int64_t(hkv) * D + cv * 8;
+
+  float acc[G][T::DL];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int j = 0; j < T::DL; ++j) acc[h][j] = 0.f;
+  float mh[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) mh[h] = -INFINITY;
+  float lrow[4] = {0.f, 0.f, 0.f, 0.f};
+  const int row = lane >> 4;  // S-layout row group: heads 4*row .. 4*row+3
+
+  for (int base = it.page_begin; base < it.page_end; base += 64) {
+    const int nblk = min(64, it.page_end - base);
+    const int pid = (lane < nblk) ? p.indices[base + lane] : 0;
+    uint4 kn[T::KSTEPS], vn[T::PASSES][T::VL];
+    auto load_page = [&](int page) {
+      if (page < 0 || page >= p.num_pages) {  // invalid page id: read nothing, contribute zeros
+#pragma unroll
+        for (int s = 0; s < T::KSTEPS; ++s) kn[s] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int ps = 0; ps < T::PASSES; ++ps)
+#pragma unroll
+          for (int j = 0; j < T::VL; ++j) vn[ps][j] = make_uint4(0, 0, 0, 0);
+        return;
+      }
+      const uint16_t* pg = p.pool + int64_t(page) * page_stride;
+#pragma unroll
+      for (int s = 0; s < T::KSTEPS; ++s) kn[s] = mi::load16(pg + k_off + s * 32);
+#pragma unroll
+      for (int ps = 0; ps < T::PASSES; ++ps)
+#pragma unroll
+        for (int j = 0; j < T::VL; ++j)
+          vn[ps][j] = mi::load16(pg + v_off + int64_t(ps * T::TPP) * tok_stride + j * (T::LPT * 8));
+    };
+    load_page(mi::read_lane_i(pid, 0));
+    for (int k = 0; k < nblk; ++k) {
+      uint4 kc[T::KSTEPS], vc[T::PASSES][T::VL];
+#pragma unroll
+      for (int s = 0; s < T::KSTEPS; ++s) kc[s] = kn[s];
+#pragma unroll
+      for (int ps = 0; ps < T::PASSES; ++ps)
+#pragma unroll
+        for (int j = 0; j < T::VL; ++j) vc[ps][j] = vn[ps][j];
+      if (k + 1 < nblk) load_page(mi::read_lane_i(pid, k + 1));
+      const int valid = (base + k == it.page_end - 1) ? it.last_valid : kPageSize;
+
+      // ---- S = Q K^T (lane: heads 4*row+i, token lane&15)
+      mi::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < T::KSTEPS; ++s) c = mi::mfma_16x16x32_bf16(qa[s], mi::as_bf16x8(kc[s]), c);
+      const int tok = lane & 15;
+      float s2[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s2[i] = (tok < valid) ? c[i] * p.scale_log2 : -INFINITY;
+
+      // ---- page max per head, lazy rescale
+      float rm[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rm[i] = mi::group16_max(s2[i]);
+      float mp[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) mp[h] = mi::read_lane(rm[h & 3], (h >> 2) * 16);
+      bool need = false;
+#pragma unroll
+      for (int h = 0; h < G; ++h) need |= (mp[h] > mh[h] + kLazyRescale);
+      if (need) {
+        float f[8];
+#pragma unroll
+        for (int h = 0; h < 8; ++h) f[h] = 1.f;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          if (mp[h] > mh[h] + kLazyRescale) {
+            f[h] = (mh[h] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mh[h] - mp[h]);
+            mh[h] = mp[h];
+#pragma unroll
+            for (int j = 0; j < T::DL; ++j) acc[h][j] *= f[h];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lrow[i] *= (row == 0) ? f[i] : f[4 + i];
+      }
+      float pS[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float mm = 0.f;
+        if (i < G) mm = mh[i];
+        if (row == 1 && 4 + i < G) mm = mh[(4 + i < G) ? 4 + i : 0];
+        pS[i] = __builtin_amdgcn_exp2f(s2[i] - mm);
+        lrow[i] += pS[i];
+      }
+
+      // ---- O += P V
+#pragma unroll
+      for (int ps = 0; ps < T::PASSES; ++ps) {
+        const int tsrc = tv + ps * T::TPP;
+        float pv[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) pv[h] = mi::lane_shuffle(pS[h & 3], (h >> 2) * 16 + tsrc);
+        const bool vmask = tsrc >= valid;
+#pragma unroll
+        for (int j = 0; j < T::VL; ++j) {
+          uint4 v = vc[ps][j];
+          if (vmask) v = make_uint4(0, 0, 0, 0);
+          float vf[8] = {mi::bf16_lo(v.x), mi::bf16_hi(v.x), mi::bf16_lo(v.y), mi::bf16_hi(v.y),
+                         mi::bf16_lo(v.z), mi::bf16_hi(v.z), mi::bf16_lo(v.w), mi::bf16_hi(v.w)};
+#pragma unroll
+          for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[h][j * 8 + e] = fmaf(pv[h], vf[e], acc[h][j * 8 + e]);
+        }
+      }
+    }
+  }
+
+  // ---- softmax denominators (wave-uniform per head)
+  float lh[G];
+  {
+    float ls[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ls[i] = mi::group16_sum(lrow[i]);
+#pragma unroll
+    for (int h = 0; h < G; ++h) lh[h] = mi::read_lane(ls[h & 3], (h >> 2) * 16);
+  }
+
+  // ---- reduce acc over the TPP token lanes through LDS
+  float o[G][T::OUT];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+#pragma unroll
+    for (int j = 0; j < T::VL; ++j) {
+      float* dst = &red[tv][j * (T::LPT * 8) + cv * 8];
+      *reinterpret_cast<float4*>(dst) =
+          make_float4(acc[h][j * 8 + 0], acc[h][j * 8 + 1], acc[h][j * 8 + 2], acc[h][j * 8 + 3]);
+      *reinterpret_cast<float4*>(dst + 4) =
+          make_float4(acc[h][j * 8 + 4], acc[h][j * 8 + 5], acc[h][j * 8 + 6], acc[h][j * 8 + 7]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < T::OUT; ++k) {
+      float sum = 0.f;
+#pragma unroll
+      for (int t = 0; t < T::TPP; ++t) sum += red[t][lane + 64 * k];
+      o[h][k] = sum;
+    }
+    __syncthreads();
+  }
+
+  if (it.nsplit == 1) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float inv = lh[h] > 0.f ? 1.f / lh[h] : 0.f;
+      uint16_t* orow = p.out + int64_t(b) * p.o_sb + int64_t(hkv * G + h) * p.o_sh;
+#pragma unroll
+      for (int k = 0; k < T::OUT; ++k) orow[lane + 64 * k] = mi::f32_to_bf16(o[h][k] * inv);
+    }
+    return;
+  }
+
+  // ---- split-K: publish the partial, the last unit of (b, hkv) merges.
+  {
+    float* po = p.po + int64_t(u) * G * D;
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int k = 0; k < T::OUT; ++k) po[h * D + lane + 64 * k] = o[h][k];
+    if (lane < G) {
+      float mv = 0.f, lv = 0.f;
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+        if (lane == h) {
+          mv = mh[h];
+          lv = lh[h];
+        }
+      p.pml[(int64_t(u) * G + lane) * 2 + 0] = mv;
+      p.pml[(int64_t(u) * G + lane) * 2 + 1] = lv;
+    }
+  }
+  __threadfence();
+  int prev = 0;
+  int* counter = p.counters + b * p.hkv + hkv;
+  if (lane == 0)
+    prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  prev = mi::read_lane_i(prev, 0);
+  if (prev != it.nsplit - 1) return;
+  __threadfence();
+
+  const int ns = it.nsplit;
+  const int my_unit = (it.item_base + lane) * p.hkv + hkv;  // split `lane`
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float ms = -INFINITY, ls = 0.f;
+    if (lane < ns) {
+      ms = __hip_atomic_load(p.pml + (int64_t(my_unit) * G + h) * 2 + 0, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      ls = __hip_atomic_load(p.pml + (int64_t(my_unit) * G + h) * 2 + 1, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const float M = mi::wave_max(ms);
+    const float w = (lane < ns) ? __builtin_amdgcn_exp2f(ms - M) : 0.f;
+    const float Lt = mi::wave_sum(w * ls);
+    const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
+    float sum[T::OUT];
+#pragma unroll
+    for (int k = 0; k < T::OUT; ++k) sum[k] = 0.f;
+    for (int s = 0; s < ns; ++s) {
+      const float ws = mi::read_lane(w, s);
+      const int us = (it.item_base + s) * p.hkv + hkv;
+      const float* src = p.po + (int64_t(us) * G + h) * D;
+#pragma unroll
+      for (int k = 0; k < T::OUT; ++k)
+        sum[k] += ws * __hip_atomic_load(src + lane + 64 * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    uint16_t* orow = p.out + int64_t(b) * p.o_sb + int64_t(hkv * G + h) * p.o_sh;
+#pragma unroll
+    for (int k = 0; k < T::OUT; ++k) orow[lane + 64 * k] = mi::f32_to_bf16(sum[k] * inv);
+  }
+  if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(64) void decode_run_kernel(RunParams p) {
+  __shared__ float red[DecodeTraits<D, G>::TPP][D + 4];
+  const int num_units = p.header->num_units;
+  for (int u = blockIdx.x; u < num_units; u += gridDim.x) decode_unit<D, G>(p, u, red);
+}
+
+typedef void (*RunKernel)(RunParams);
+
+template <int D>
+RunKernel pick_group(int g) {
+  switch (g) {
+    case 1: return decode_run_kernel<D, 1>;
+    case 2: return decode_run_kernel<D, 2>;
+    case 3: return decode_run_kernel<D, 3>;
+    case 4: return decode_run_kernel<D, 4>;
+    case 5: return decode_run_kernel<D, 5>;
+    case 6: return decode_run_kernel<D, 6>;
+    case 7: return decode_run_kernel<D, 7>;
+    case 8: return decode_run_kernel<D, 8>;
+    default: return nullptr;
+  }
+}
+
+RunKernel pick_kernel(int head_dim, int group) {
+  switch (head_dim) {
+    case 64: return pick_group<64>(group);
+    case 128: return pick_group<128>(group);
+    case 256: return pick_group<256>(group);
+    default: return nullptr;
+  }
+}
+
+int check_shape(const char* who, int batch, int hq, int hkv, int head_dim, int page_size) {
+  if (batch < 0 || hq <= 0 || hkv <= 0)
+    return mi::fail(MI_ERR_INVALID, "%s: bad batch/head counts (%d, %d, %d)", who, batch, hq, hkv);
+  if (hq % hkv != 0)
+    return mi::fail(MI_ERR_INVALID, "%s: num_qo_heads %d not a multiple of num_kv_heads %d", who, hq, hkv);
+  if (page_size != kPageSize)
+    return mi::fail(MI_ERR_UNSUPPORTED, "%s: page_size %d (built for 16)", who, page_size);
+  if (!pick_kernel(head_dim, hq / hkv))
+    return mi::fail(MI_ERR_UNSUPPORTED, "%s: head_dim %d / group %d not built (head_dim 64/128/256, group 1..8)",
+                    who, head_dim, hq / hkv);
+  return MI_OK;
+}
+
+}  // namespace
+
+extern "C" size_t mi_decode_workspace_size(int32_t batch_size, int32_t num_qo_heads,
+                                           int32_t num_kv_heads, int32_t head_dim, int32_t max_units) {
+  if (batch_size < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || num_qo_heads % num_kv_heads) return 0;
+  if (max_units <= 0) max_units = default_max_units(batch_size, num_kv_heads);
+  return decode_layout(batch_size, num_qo_heads, num_kv_heads, head_dim, max_units).total;
+}
+
+extern "C" int mi_decode_plan(void* workspace, size_t workspace_bytes, const int32_t* kv_indptr,
+                              const int32_t* kv_last_page_len, int32_t batch_size,
+                              int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                              int32_t page_size, int32_t max_units, mi_stream_t stream) {
+  mi::clear_error();
+  int rc = check_shape("decode plan", batch_size, num_qo_heads, num_kv_heads, head_dim, page_size);
+  if (rc) return rc;
+  if (max_units <= 0) max_units = default_max_units(batch_size, num_kv_heads);
+  const DecodeLayout L = decode_layout(batch_size, num_qo_heads, num_kv_heads, head_dim, max_units);
+  if (!workspace || workspace_bytes < L.total)
+    return mi::fail(MI_ERR_WORKSPACE, "decode plan: workspace %zu bytes, need %zu", workspace_bytes, L.total);
+  if (L.max_items < batch_size)
+    return mi::fail(MI_ERR_INVALID, "decode plan: max_units %d below batch*kv_heads %d", max_units,
+                    batch_size * num_kv_heads);
+  if (batch_size > 0 && (!kv_indptr || !kv_last_page_len))
+    return mi::fail(MI_ERR_INVALID, "decode plan: null indptr / last_page_len");
+  char* ws = static_cast<char*>(workspace);
+  PlanParams pp;
+  pp.indptr = kv_indptr;
+  pp.last_page_len = kv_last_page_len;
+  pp.batch = batch_size;
+  pp.hkv = num_kv_heads;
+  pp.target_units = mi::num_cus() * kUnitsPerCU;
+  pp.max_items = L.max_items;
+  pp.header = reinterpret_cast<DecodeHeader*>(ws);
+  pp.items = reinterpret_cast<DecodeItem*>(ws + L.items);
+  pp.counters = reinterpret_cast<int*>(ws + L.counters);
+  hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream), pp);
+  return mi::check_launch("decode_plan_kernel");
+}
+
+extern "C" int mi_decode_run(void* workspace, size_t workspace_bytes, const void* q,
+                             int64_t q_stride_batch, int64_t q_stride_head, const void* paged_kv_cache,
+                             int64_t num_pages, const int32_t* kv_indices, void* out,
+                             int64_t out_stride_batch, int64_t out_stride_head, int32_t batch_size,
+                             int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                             int32_t page_size, float sm_scale, int32_t max_units, mi_stream_t stream) {
+  mi::clear_error();
+  int rc = check_shape("decode run", batch_size, num_qo_heads, num_kv_heads, head_dim, page_size);
+  if (rc) return rc;
+  if (batch_size == 0) return MI_OK;
+  if (max_units <= 0) max_units = default_max_units(batch_size, num_kv_heads);
+  const DecodeLayout L = decode_layout(batch_size, num_qo_heads, num_kv_heads, head_dim, max_units);
+  if (!workspace || workspace_bytes < L.total)
+    return mi::fail(MI_ERR_WORKSPACE, "decode run: workspace %zu bytes, need %zu", workspace_bytes, L.total);
+  if (!q || !paged_kv_cache || !kv_indices || !out)
+    return mi::fail(MI_ERR_INVALID, "decode run: null pointer argument");
+  if ((reinterpret_cast<uintptr_t>(q) & 15) || (reinterpret_cast<uintptr_t>(paged_kv_cache) & 15) ||
+      q_stride_batch % 8 || q_stride_head % 8)
+    return mi::fail(MI_ERR_INVALID, "decode run: q rows and pool must be 16-byte aligned");
+  char* ws = static_cast<char*>(workspace);
+  RunParams rp;
+  rp.header = reinterpret_cast<const DecodeHeader*>(ws);
+  rp.items = reinterpret_cast<const DecodeItem*>(ws + L.items);
+  rp.counters = reinterpret_cast<int*>(ws + L.counters);
+  rp.pml = reinterpret_cast<float*>(ws + L.pml);
+  rp.po = reinterpret_cast<float*>(ws + L.po);
+  rp.q = static_cast<const uint16_t*>(q);
+  rp.q_sb = q_stride_batch;
+  rp.q_sh = q_stride_head;
+  rp.pool = static_cast<const uint16_t*>(paged_kv_cache);
+  rp.num_pages = num_pages;
+  rp.indices = kv_indices;
+  rp.out = static_cast<uint16_t*>(out);
+  rp.o_sb = out_stride_batch;
+  rp.o_sh = out_stride_head;
+  rp.hkv = num_kv_heads;
+  const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf(float(head_dim));
+  rp.scale_log2 = scale * mi::kLog2e;
+  RunKernel k = pick_kernel(head_dim, num_qo_heads / num_kv_heads);
+  const int grid = min(max_units, mi::num_cus() * kUnitsPerCU);
+  hipLaunchKernelGGL(k, dim3(grid), dim3(64), 0, static_cast<hipStream_t>(stream), rp);
+  return mi::check_launch("decode_run_kernel");
+}

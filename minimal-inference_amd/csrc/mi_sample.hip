@@ -1,0 +1,275 @@
+// Fused batched sampler: greedy argmax, temperature, top-p, multinomial.
+//
+// Reference: sample_batch (scheduler.py:319-343) and sample (310-316).
+//   * temperatures are held in the logits dtype, i.e. rounded to bf16 (327);
+//   * rows with temperature <= 0 take argmax(logits), first index on ties
+//     (328, 339-341); NaN ranks above every number, as in torch.argmax;
+//   * other rows draw from softmax(bf16(logit / clamp(t, 1e-6))) in fp32
+//     (331-336).  top-p (an extension) keeps the smallest set of most likely
+//     tokens whose mass reaches top_p, ties at the boundary included.
+//
+// One 1024-thread workgroup per row.  The draw is an exponential race
+// (Gumbel-max): argmax_i (s_i * log2 e - log2(-log2 u_i)), which selects i with
+// probability proportional to exp(s_i); u_i comes from Philox4x32-10 (Salmon,
+// Moraes, Dror, Shaw, "Parallel random numbers: as easy as 1, 2, 3", SC 2011)
+// with counter (token / 4, row, offset) and key = seed.  The top-p boundary
+// is found exactly on the 16-bit bf16 key of s_i with four 4-bit radix passes
+// of probability mass (per-thread LDS bins, no atomics), so no sort is needed.
+#include <math.h>
+
+#include "mi_common.h"
+
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr uint32_t kNaNKey = 0x10000u;
+
+// Order-preserving 16-bit key of a bf16 value; -0 and +0 share a key and NaN
+// (either sign) ranks above +inf.
+__device__ __forceinline__ uint32_t bf16_key(uint16_t b) {
+  if ((b & 0x7fffu) > 0x7f80u) return kNaNKey;
+  if (b == 0x8000u) b = 0;
+  return (b & 0x8000u) ? (~uint32_t(b) & 0xffffu) : (uint32_t(b) | 0x8000u);
+}
+
+__device__ __forceinline__ float key_to_f32(uint32_t k) {
+  const uint32_t b = (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu);
+  return __uint_as_float(b << 16);
+}
+
+// Philox4x32-10 (Salmon et al. 2011): multipliers 0xD2511F53 / 0xCD9E8D57,
+// Weyl key increments 0x9E3779B9 / 0xBB67AE85.
+__device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint2 k) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t lo0 = 0xD2511F53u * c.x, hi0 = __umulhi(0xD2511F53u, c.x);
+    const uint32_t lo1 = 0xCD9E8D57u * c.z, hi1 = __umulhi(0xCD9E8D57u, c.z);
+    c = make_uint4(hi1 ^ c.y ^ k.x, lo1, hi0 ^ c.w ^ k.y, lo0);
+    k.x += 0x9E3779B9u;
+    k.y += 0xBB67AE85u;
+  }
+  return c;
+}
+
+// Uniform in (0, 1) from 24 random bits.
+__device__ __forceinline__ float u01(uint32_t x) { return (float(x >> 8) + 0.5f) * (1.0f / 16777216.0f); }
+
+struct SampleParams {
+  const uint16_t* logits;
+  int64_t stride;
+  int batch, vocab;
+  const float* temperature;
+  const float* top_p;
+  uint2 seed;
+  const uint64_t* offset;
+  int64_t* out;
+};
+
+// (key, index) argmax: larger key wins, lower index breaks ties.
+__device__ __forceinline__ void better(uint32_t& bk, int& bi, uint32_t k, int i) {
+  if (k > bk || (k == bk && i < bi)) {
+    bk = k;
+    bi = i;
+  }
+}
+__device__ __forceinline__ void betterf(float& bv, int& bi, float v, int i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+template <typename F>
+__device__ __forceinline__ void block_argmax(F& bv, int& bi, F* sv, int* si) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int o = 32; o > 0; o >>= 1) {
+    F ov;
+    if constexpr (sizeof(F) == 4 && (F(0.5) != F(0))) {
+      ov = __shfl_xor(bv, o);
+    } else {
+      ov = F(__shfl_xor(int(bv), o));
+    }
+    const int oi = __shfl_xor(bi, o);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  __syncthreads();
+  if (lane == 0) {
+    sv[w] = bv;
+    si[w] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < kThreads / 64; ++k)
+      if (sv[k] > sv[0] || (sv[k] == sv[0] && si[k] < si[0])) {
+        sv[0] = sv[k];
+        si[0] = si[k];
+      }
+  }
+  __syncthreads();
+  bv = sv[0];
+  bi = si[0];
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams p) {
+  __shared__ float bins[16 * kThreads];  // per-thread private radix bins
+  __shared__ float bin_tot[16];
+  __shared__ uint32_t sh_u[16];
+  __shared__ float sh_f[16];
+  __shared__ int sh_i[16];
+  __shared__ uint32_t sh_prefix;
+  __shared__ float sh_above, sh_target;
+
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const uint16_t* x = p.logits + int64_t(row) * p.stride;
+  const int V = p.vocab;
+
+  const uint16_t tb = mi::f32_to_bf16(p.temperature[row]);
+  const float tq = mi::bf16_to_f32(tb);
+  const bool greedy = !(tq > 0.f);  // <= 0 (and NaN) is greedy
+
+  if (greedy) {
+    uint32_t bk = 0;
+    int bi = 0x7fffffff;
+    for (int i = tid; i < V; i += kThreads) better(bk, bi, bf16_key(x[i]), i);
+    block_argmax<uint32_t>(bk, bi, sh_u, sh_i);
+    if (tid == 0) p.out[row] = bi < V ? bi : 0;
+    return;
+  }
+
+  // clamp(min=1e-6) in bf16, then s_i = bf16(logit_i / t)
+  const float tmin = mi::bf16_to_f32(mi::f32_to_bf16(1e-6f));
+  const float tc = fmaxf(tq, tmin);
+  auto scaled = [&](int i) -> uint16_t { return mi::f32_to_bf16(mi::bf16_to_f32(x[i]) / tc); };
+
+  // ---- max key
+  uint32_t mk = 0;
+  {
+    int unused = 0;
+    for (int i = tid; i < V; i += kThreads) better(mk, unused, bf16_key(scaled(i)), 0);
+    block_argmax<uint32_t>(mk, unused, sh_u, sh_i);
+  }
+  const float smax = key_to_f32(mk) * mi::kLog2e;
+
+  uint32_t kstar = 0;
+  const float tp = p.top_p ? p.top_p[row] : 1.0f;
+  if (tp < 1.0f && mk != kNaNKey) {
+    uint32_t prefix = 0;
+    if (tid == 0) sh_above = 0.f;
+    for (int pass = 0; pass < 4; ++pass) {
+      const int shift = 12 - 4 * pass;
+#pragma unroll
+      for (int d = 0; d < 16; ++d) bins[d * kThreads + tid] = 0.f;
+      for (int i = tid; i < V; i += kThreads) {
+        const uint32_t k = bf16_key(scaled(i));
+        if (k == kNaNKey) continue;
+        if (pass > 0 && (k >> (shift + 4)) != prefix) continue;
+        const float mass = __builtin_amdgcn_exp2f(key_to_f32(k) * mi::kLog2e - smax);
+        bins[((k >> shift) & 15) * kThreads + tid] += mass;
+      }
+      __syncthreads();
+      {
+        const int w = tid >> 6, lane = tid & 63;  // wave w sums digit w
+        float s = 0.f;
+        for (int j = lane; j < kThreads; j += 64) s += bins[w * kThreads + j];
+        s = mi::wave_sum(s);
+        if (lane == 0) bin_tot[w] = s;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        if (pass == 0) {
+          float z = 0.f;
+          for (int d = 0; d < 16; ++d) z += bin_tot[d];
+          sh_target = tp * z;
+        }
+        float above = sh_above;
+        int pick = -1, lowest = -1;
+        for (int d = 15; d >= 0; --d) {
+          if (bin_tot[d] <= 0.f) continue;
+          lowest = d;
+          if (above + bin_tot[d] >= sh_target) {
+            pick = d;
+            break;
+          }
+          above += bin_tot[d];
+        }
+        if (pick < 0) {  // rounding left the target unreached: take the last digit
+          pick = lowest < 0 ? 0 : lowest;
+          above = sh_above;
+          for (int d = 15; d > pick; --d) above += bin_tot[d];
+        }
+        sh_above = above;
+        sh_prefix = (prefix << 4) | uint32_t(pick);
+      }
+      __syncthreads();
+      prefix = sh_prefix;
+      __syncthreads();
+    }
+    kstar = prefix;
+  }
+
+  // ---- exponential race over the kept tokens
+  const uint64_t off = *p.offset;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int g = tid; g * 4 < V; g += kThreads) {
+    const uint4 r = philox4x32_10(make_uint4(uint32_t(g), uint32_t(row), uint32_t(off), uint32_t(off >> 32)), p.seed);
+    const uint32_t rr[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 4 * g + e;
+      if (i >= V) break;
+      const uint32_t k = bf16_key(scaled(i));
+      if (k < kstar) continue;
+      float v;
+      if (k == kNaNKey) {
+        v = INFINITY;
+      } else {
+        const float s = key_to_f32(k);
+        if (s == -INFINITY) continue;
+        v = s * mi::kLog2e - __log2f(-__log2f(u01(rr[e])));
+      }
+      betterf(bv, bi, v, i);
+    }
+  }
+  block_argmax<float>(bv, bi, sh_f, sh_i);
+  if (tid == 0) p.out[row] = bi < V ? bi : 0;
+}
+
+__global__ void advance_offset_kernel(uint64_t* off) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) off[0] += 1;
+}
+
+}  // namespace
+
+extern "C" int mi_sample(const void* logits, int64_t logits_row_stride, int32_t batch_size,
+                         int32_t vocab_size, const float* temperature, const float* top_p,
+                         uint64_t seed, uint64_t* rng_offset, int64_t* out_tokens, mi_stream_t stream) {
+  mi::clear_error();
+  if (batch_size < 0 || vocab_size <= 0 || logits_row_stride < vocab_size)
+    return mi::fail(MI_ERR_INVALID, "sample: bad sizes (batch %d, vocab %d, stride %lld)", batch_size,
+                    vocab_size, (long long)logits_row_stride);
+  if (batch_size == 0) return MI_OK;
+  if (!logits || !temperature || !rng_offset || !out_tokens)
+    return mi::fail(MI_ERR_INVALID, "sample: null pointer argument");
+  SampleParams sp;
+  sp.logits = static_cast<const uint16_t*>(logits);
+  sp.stride = logits_row_stride;
+  sp.batch = batch_size;
+  sp.vocab = vocab_size;
+  sp.temperature = temperature;
+  sp.top_p = top_p;
+  sp.seed = make_uint2(uint32_t(seed), uint32_t(seed >> 32));
+  sp.offset = rng_offset;
+  sp.out = out_tokens;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(sample_kernel, dim3(batch_size), dim3(kThreads), 0, s, sp);
+  int rc = mi::check_launch("sample_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(advance_offset_kernel, dim3(1), dim3(64), 0, s, rng_offset);
+  return mi::check_launch("advance_offset_kernel");
+}

@@ -1,0 +1,17 @@
+"""CPU oracle for the ragged paged-attention path -- TEST INFRASTRUCTURE ONLY.
+
+This package restates, on the CPU, the arithmetic of the reference's
+paged-attention hot path so that the HIP kernels can be checked against it.
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import it, and only as the checker (or the timed CPU
+baseline); the product package never imports it and has no CPU fallback.
+
+Modules:
+  paging     -- page pool layout, FIFO page allocator replay, CSR builder,
+                KV append (integer / byte exact).
+  attention  -- gather-based paged decode and causal prefill attention in fp32.
+  sampling   -- greedy argmax, bf16 temperature quantisation, the fp32
+                (top-p restricted) sampling distribution.
+
+Pinning status per function is recorded in each module's docstring.
+"""

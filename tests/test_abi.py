@@ -1,0 +1,58 @@
+"""CPU: the C-ABI library loads and exports every entry point the header declares."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "mi_amd.h"
+
+
+def declared_symbols() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(mi_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_declares_the_path():
+    syms = declared_symbols()
+    for s in ("mi_paged_kv_append", "mi_decode_plan", "mi_decode_run", "mi_prefill_plan",
+              "mi_prefill_run", "mi_sample", "mi_page_table_step", "mi_last_error"):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol():
+    from minimal_inference_amd import _lib
+
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [s for s in sorted(declared_symbols()) if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_python_prototypes_match_header():
+    from minimal_inference_amd import _lib
+
+    assert set(_lib.SIGNATURES) == declared_symbols()
+
+
+def test_host_only_calls_and_error_reporting():
+    """Size queries and argument validation run without touching a GPU."""
+    from minimal_inference_amd import _lib
+
+    lib = _lib.load()
+    assert lib.mi_version() >= 100
+    assert lib.mi_decode_workspace_size(32, 32, 8, 128, 4096) > 0
+    assert lib.mi_decode_workspace_size(4, 30, 8, 128, 0) == 0  # 30 % 8 != 0
+    assert lib.mi_prefill_workspace_size(8, 4096) > 0
+    assert lib.mi_page_table_state_size(1024, 8, 64) > 0
+    # invalid arguments are rejected before any launch
+    rc = lib.mi_paged_kv_append(None, 0, 0, None, 0, 0, None, None, 1, None, 0, None, None, None,
+                                1, 2, 64, 16, None)
+    assert rc == _lib.MI_ERR_INVALID
+    assert "append" in _lib.last_error()
+    rc = lib.mi_decode_plan(None, 0, None, None, 1, 32, 8, 96, 16, 0, None)
+    assert rc == _lib.MI_ERR_UNSUPPORTED
+    rc = lib.mi_decode_plan(None, 0, None, None, 1, 32, 8, 128, 16, 0, None)
+    assert rc == _lib.MI_ERR_WORKSPACE

@@ -1,0 +1,202 @@
+"""GPU parity: split-K paged decode attention vs the fp32 oracle.
+
+Tolerance: max-abs 2e-2 against the fp32 oracle on bf16 inputs (the output is
+bf16, whose rounding alone is up to 2^-9 relative).
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from oracle import attention as oatt
+from tests.helpers import make_paged_batch, to_dev
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _wrapper(dev, ws_mb=128):
+    from minimal_inference_amd.decode import BatchDecodeWithPagedKVCacheWrapper
+
+    ws = torch.empty(ws_mb << 20, dtype=torch.uint8, device=dev)
+    return BatchDecodeWithPagedKVCacheWrapper(ws, kv_layout="NHD")
+
+
+def _decode(dev, batch, hq, hkv, d, w=None):
+    pool, q, ip, ix, lp = to_dev(batch, dev)
+    w = w or _wrapper(dev)
+    w.plan(ip, ix, lp, hq, hkv, d, 16, pos_encoding_mode="NONE", q_data_type=torch.bfloat16,
+           data_type=torch.bfloat16)
+    out = w.run(q, pool)
+    torch.cuda.synchronize()
+    return out.float().cpu()
+
+
+def _ref(batch):
+    return oatt.decode(batch["q"], batch["pool"], batch["indptr"], batch["indices"].tolist(), batch["last"])
+
+
+def test_config1_qwen05_heads(dev):
+    """Qwen2.5-0.5B heads (14/2, d=64), contexts {17, 64, 203, 511}, seed 0."""
+    b = make_paged_batch([17, 64, 203, 511], 14, 2, 64, num_pages=128, seed=0)
+    err = (_decode(dev, b, 14, 2, 64) - _ref(b)).abs().max().item()
+    assert err < TOL, err
+
+
+@pytest.mark.parametrize("hq,hkv,d", [
+    (32, 8, 128),   # Mistral-7B, group 4
+    (28, 4, 128),   # Qwen2.5-7B, group 7 (no padding)
+    (64, 8, 128),   # Qwen2.5-72B, group 8
+    (14, 2, 64),    # Qwen2.5-0.5B, group 7
+    (8, 8, 128),    # group 1
+    (12, 4, 64),    # group 3
+    (10, 2, 128),   # group 5
+    (12, 2, 128),   # group 6
+    (4, 2, 64),     # group 2
+    (16, 4, 256),   # head_dim 256
+])
+def test_shapes_ragged(dev, hq, hkv, d):
+    lens = [1, 15, 16, 17, 33, 100, 257, 700]
+    b = make_paged_batch(lens, hq, hkv, d, seed=hq * 7 + d)
+    err = (_decode(dev, b, hq, hkv, d) - _ref(b)).abs().max().item()
+    assert err < TOL, err
+
+
+def test_mistral_b32_ragged(dev):
+    """Mistral-7B decode shape: B=32, contexts U[128,1024] + 25, seed 2."""
+    g = torch.Generator().manual_seed(2)
+    lens = (torch.randint(128, 1025, (32,), generator=g) + 25).tolist()
+    b = make_paged_batch(lens, 32, 8, 128, seed=2)
+    err = (_decode(dev, b, 32, 8, 128) - _ref(b)).abs().max().item()
+    assert err < TOL, err
+
+
+@pytest.mark.parametrize("ctx", [4096, 16384])
+def test_long_context_many_splits(dev, ctx):
+    """One request: the split-K merge across up to 64 splits."""
+    b = make_paged_batch([ctx], 28, 4, 128, seed=ctx)
+    err = (_decode(dev, b, 28, 4, 128) - _ref(b)).abs().max().item()
+    assert err < TOL, err
+
+
+def test_empty_request_gives_zero(dev):
+    b = make_paged_batch([0, 40], 8, 2, 64, seed=5)
+    out = _decode(dev, b, 8, 2, 64)
+    assert torch.count_nonzero(out[0]) == 0
+    assert (out[1] - _ref(b)[1]).abs().max().item() < TOL
+
+
+def test_single_token_returns_v0(dev):
+    """kv_len = 1: softmax weight 1 on the only token, so out == V[0] exactly."""
+    b = make_paged_batch([1, 1, 1], 32, 8, 128, seed=11)
+    out = _decode(dev, b, 32, 8, 128)
+    for r in range(3):
+        page = int(b["indices"][r])
+        v0 = b["pool"][page, 1, 0].float()  # [hkv, d]
+        assert torch.equal(out[r], v0.repeat_interleave(4, dim=0))
+
+
+def test_constant_keys_average_values(dev):
+    """Identical keys give uniform weights: out == mean(V) over the context."""
+    b = make_paged_batch([48, 130], 16, 4, 128, seed=13)
+    b["pool"][:, 0] = b["pool"][0, 0, 0]  # every key row identical
+    out = _decode(dev, b, 16, 4, 128)
+    from oracle.paging import gather_kv
+
+    for r in range(2):
+        _, v = gather_kv(b["pool"], b["indptr"], b["indices"].tolist(), b["last"], r)
+        mean = v.float().mean(dim=0).repeat_interleave(4, dim=0)
+        assert (out[r] - mean).abs().max().item() < 1e-2
+
+
+def test_plan_once_run_many_layers(dev):
+    """One plan serves several layer pools (the per-step pattern)."""
+    lens = [300, 17, 900, 64]
+    w = _wrapper(dev)
+    batches = [make_paged_batch(lens, 32, 8, 128, seed=100 + i) for i in range(3)]
+    # same page table for every layer
+    for x in batches[1:]:
+        x["indices"], x["indptr"], x["last"] = batches[0]["indices"], batches[0]["indptr"], batches[0]["last"]
+    pool0, q0, ip, ix, lp = to_dev(batches[0], dev)
+    w.plan(ip, ix, lp, 32, 8, 128, 16)
+    for x in batches:
+        out = w.run(x["q"].to(dev), x["pool"].to(dev)).float().cpu()
+        assert (out - _ref(x)).abs().max().item() < TOL
+
+
+def test_strided_q_and_out(dev):
+    """q as a column slice of a fused projection; out written into a view."""
+    lens = [40, 123]
+    b = make_paged_batch(lens, 16, 4, 64, seed=21)
+    pool, _, ip, ix, lp = to_dev(b, dev)
+    big = torch.zeros(len(lens), 24 * 64, dtype=torch.bfloat16, device=dev)
+    big[:, :16 * 64] = b["q"].reshape(len(lens), -1).to(dev)
+    qv = big[:, :16 * 64].view(len(lens), 16, 64)
+    outbuf = torch.zeros(len(lens), 20 * 64, dtype=torch.bfloat16, device=dev)
+    ov = outbuf[:, 64:17 * 64].view(len(lens), 16, 64)
+    w = _wrapper(dev)
+    w.plan(ip, ix, lp, 16, 4, 64, 16)
+    w.run(qv, pool, out=ov)
+    torch.cuda.synchronize()
+    assert (ov.float().cpu() - _ref(b)).abs().max().item() < TOL
+    assert torch.count_nonzero(outbuf[:, :64]) == 0
+
+
+def test_graph_replay_after_replan(dev):
+    """run() captured once replays correctly after every later plan()."""
+    hq, hkv, d = 32, 8, 128
+    w = _wrapper(dev)
+    cap = 256
+    ip = torch.zeros(5, dtype=torch.int32, device=dev)
+    ix = torch.zeros(cap, dtype=torch.int32, device=dev)
+    lp = torch.ones(4, dtype=torch.int32, device=dev)
+    q = torch.zeros(4, hq, d, dtype=torch.bfloat16, device=dev)
+    pool = torch.zeros(300, 2, 16, hkv, d, dtype=torch.bfloat16, device=dev)
+    out = torch.zeros(4, hq, d, dtype=torch.bfloat16, device=dev)
+    first = make_paged_batch([16, 16, 16, 16], hq, hkv, d, num_pages=300, seed=1)
+    ip.copy_(torch.tensor(first["indptr"], dtype=torch.int32))
+    ix[:4].copy_(first["indices"])
+    w.plan(ip, ix, lp, hq, hkv, d, 16)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        w.run(q, pool, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        w.run(q, pool, out=out)
+    for seed, lens in [(2, [100, 5, 700, 33]), (3, [1, 1000, 64, 250]), (4, [3000, 1, 2, 17])]:
+        b = make_paged_batch(lens, hq, hkv, d, num_pages=300, seed=seed)
+        pool.copy_(b["pool"])
+        q.copy_(b["q"])
+        ip.copy_(torch.tensor(b["indptr"], dtype=torch.int32))
+        ix[: b["indices"].numel()].copy_(b["indices"])
+        lp.copy_(torch.tensor(b["last"], dtype=torch.int32))
+        w.plan(ip, ix, lp, hq, hkv, d, 16)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.float().cpu()
+        eager = w.run(q, pool).float().cpu()
+        assert torch.equal(got, eager)
+        assert (got - _ref(b)).abs().max().item() < TOL
+
+
+def test_rejects_unsupported(dev):
+    w = _wrapper(dev)
+    ip = torch.tensor([0, 1], dtype=torch.int32, device=dev)
+    ix = torch.zeros(1, dtype=torch.int32, device=dev)
+    lp = torch.ones(1, dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError):
+        w.plan(ip, ix, lp, 32, 8, 96, 16)  # head_dim 96 not built
+    with pytest.raises(ValueError):
+        w.plan(ip, ix, lp, 18, 2, 128, 16)  # group 9
+    with pytest.raises(ValueError):
+        w.plan(ip, ix, lp, 32, 8, 128, 16, pos_encoding_mode="ROPE_LLAMA")
+    with pytest.raises(RuntimeError):
+        from minimal_inference_amd.decode import BatchDecodeWithPagedKVCacheWrapper
+
+        small = BatchDecodeWithPagedKVCacheWrapper(torch.empty(1024, dtype=torch.uint8, device=dev))
+        small.plan(ip, ix, lp, 32, 8, 128, 16)
