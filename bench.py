@@ -1,0 +1,197 @@
+"""Benchmark: decode tok/s and decode-attention HBM GB/s, Mistral-7B, B=32, one GPU.
+
+Workload (random-initialised Mistral-7B architecture, bf16): 32 concurrent
+requests with prompt lengths uniform in [128, 1024] and random token ids
+(seed 2); even requests greedy, odd ones temperature 0.7 / top-p 0.9;
+page_size 16; one hipGraph per decode batch size.  All prompts are admitted
+and prefilled (one ragged batch) before timing.
+
+A "step" is one full decode step of the 32-request batch: device page-table
+step, plan(), graph replay (32 layers: GEMMs, RoPE, KV append, split-K paged
+attention, sampler) and the read-back of the sampled ids.  ``value`` is
+decoded tokens per second over exactly ``--steps`` timed steps.
+
+``roofline`` is measured on the decode-attention kernel alone: after the
+timed steps, the 32 layers' attention (the batch's real page tables and
+pools) is launched ``--attn-iters`` times on the current stream and bracketed
+with HIP events; achieved = algorithmic bytes per launch / average launch
+time.  ``cpu_baseline`` times the CPU oracle's gather-based attention on one
+layer of the same batch.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBPS = 8000.0
+PUBLISHED_TOKS = 1532.0  # reference README.md:56, H100, 32 concurrent, aggregate tok/s
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--model", default="mistral-7b")
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--seed", type=int, default=2)
+    ap.add_argument("--attn-iters", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the path runs on one MI355X); --gpus {args.gpus} "
+              "is not supported", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from __graft_entry__ import load_package
+
+    load_package()
+    from minimal_inference_amd.engine import Request, Scheduler
+    from minimal_inference_amd.model import PRESETS, Model
+
+    dev = torch.device("cuda:0")
+    cfg = PRESETS[args.model]
+    B = args.batch
+    new_tokens = max(50, args.warmup + args.steps + 1)
+    g = torch.Generator().manual_seed(args.seed)
+    lens = torch.randint(128, 1025, (B,), generator=g).tolist()
+    prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist() for n in lens]
+    max_seq = 1024 + new_tokens + 16
+
+    log(f"init {args.model} (random weights) on {torch.cuda.get_device_name(0)}")
+    t0 = time.time()
+    model = Model(cfg, dev, seed=args.seed, max_positions=max_seq + 16)
+    torch.cuda.synchronize()
+    log(f"weights {model.weight_bytes() / 1e9:.2f} GB in {time.time() - t0:.1f}s; capturing graphs")
+    sch = Scheduler(model, max_batch_size=B, max_seq_len=max_seq, seed=args.seed)
+    reqs = [Request(str(i), p, new_tokens, 0.0 if i % 2 == 0 else 0.7, 1.0 if i % 2 == 0 else 0.9)
+            for i, p in enumerate(prompts)]
+    for r in reqs:
+        sch.submit(r)
+    t0 = time.time()
+    sch.step()  # admit + ragged prefill of all 32 prompts + first decode step
+    torch.cuda.synchronize()
+    log(f"prefill + first decode step {time.time() - t0:.2f}s; warmup {args.warmup} steps")
+    for _ in range(args.warmup):
+        sch.step()
+    torch.cuda.synchronize()
+    n_active = sum(1 for r in reqs if r.status.value == "decoding")
+    if n_active != B:
+        raise RuntimeError(f"expected {B} decoding requests, have {n_active}")
+    log(f"timing {args.steps} decode steps at B={B}")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        sch.step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    toks = B * args.steps / elapsed
+    ms_step = elapsed * 1000 / args.steps
+    log(f"decode: {toks:.0f} tok/s, {ms_step:.3f} ms/step")
+
+    # ---------------- decode-attention kernel on the batch's real state
+    hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    kv_lens = [r.current_position for r in reqs]  # tokens in the cache after the last step
+    rows = [(r.slot, r.current_position - 1) for r in reqs]
+    # rebuild the CSR for exactly these contexts (no growth: pages already held)
+    sch.pt.step([], rows, B, sch.d_indptr, sch.d_indices, sch.d_last, sch.d_batch, sch.d_pos)
+    w = sch.decode_wrapper
+    w.plan(sch.d_indptr[: B + 1], sch.d_indices, sch.d_last[:B], hq, hkv, d, 16)
+    qs = [torch.randn(B, hq, d, device=dev, dtype=torch.bfloat16) for _ in range(cfg.num_hidden_layers)]
+    outs = [torch.empty_like(q) for q in qs]
+    npages = [math.ceil(n / 16) for n in kv_lens]
+    alg_bytes = sum(kv_lens) * hkv * d * 2 * 2 + 2 * B * hq * d * 2 + 4 * ((B + 1) + sum(npages) + B)
+    for _ in range(2):
+        for l in range(cfg.num_hidden_layers):
+            w.run(qs[l], sch.kv.kv_data[l], out=outs[l])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.attn_iters):
+        for l in range(cfg.num_hidden_layers):
+            w.run(qs[l], sch.kv.kv_data[l], out=outs[l])
+    e1.record(stream)
+    e1.synchronize()
+    launches = args.attn_iters * cfg.num_hidden_layers
+    attn_us = e0.elapsed_time(e1) * 1000 / launches
+    achieved = alg_bytes / (attn_us * 1e-6) / 1e9
+    log(f"decode attention: {attn_us:.2f} us/launch, {achieved:.0f} GB/s "
+        f"({100 * achieved / PEAK_HBM_GBPS:.1f}% of {PEAK_HBM_GBPS:.0f}), {alg_bytes / 1e6:.1f} MB/launch")
+
+    # ---------------- CPU baseline: the oracle on one layer of the same batch
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import attention as oatt  # CPU checker, timed as the baseline
+
+        torch.set_num_threads(max(1, min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")))))
+        ip = sch.d_indptr[: B + 1].cpu().tolist()
+        ix = sch.d_indices[: ip[-1]].cpu()
+        used = torch.unique(ix)
+        remap = {int(p): i for i, p in enumerate(used.tolist())}
+        pool_cpu = sch.kv.kv_data[0].index_select(0, used.to(dev)).cpu()
+        ix_local = [remap[int(p)] for p in ix.tolist()]
+        last = sch.d_last[:B].cpu().tolist()
+        q_cpu = qs[0].cpu()
+        for _ in range(3):
+            oatt.decode(q_cpu, pool_cpu, ip, ix_local, last)
+        times = []
+        t_budget = time.perf_counter()
+        while len(times) < 10 or (time.perf_counter() - t_budget < 10 and len(times) < 200):
+            t = time.perf_counter()
+            oatt.decode(q_cpu, pool_cpu, ip, ix_local, last)
+            times.append(time.perf_counter() - t)
+            if time.perf_counter() - t_budget > 30:
+                break
+        med = statistics.median(times)
+        cpu = {"value": round(alg_bytes / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+               "kind": "port",
+               "sample": f"oracle gather-based paged decode attention (fp32 torch) on one Mistral-7B layer of "
+                         f"this B={B} batch, median of {len(times)} runs after 3 warm-ups; "
+                         f"{med * 1000:.1f} ms per layer"}
+        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
+
+    line = {
+        "metric": "decode-attn HBM GB/s (% of peak) + decode tok/s, Mistral-7B B=32",
+        "value": round(toks, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(toks / PUBLISHED_TOKS, 4),
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, random prompt token ids)",
+        "config": {"workload": f"{args.model} decode, B={B}, prompts U[128,1024] seed {args.seed}, "
+                               f"half greedy / half T=0.7 top-p 0.9, page_size 16, hipGraph decode",
+                   "batch": B, "mean_context": round(sum(kv_lens) / B, 1), "parallelism": "single GPU"},
+        "decode_attn_us": round(attn_us, 3),
+        "decode_attn_gbps": round(achieved, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -72,24 +72,29 @@ int mi_paged_kv_append(const void* append_key, int64_t key_stride_token, int64_t
  *   plan  -- scheduler.py:402-413, 905-916, 927-938
  *   run   -- model.py:235 (mode == "decode")
  *
- * mi_decode_plan runs a one-workgroup GPU kernel that reads kv_indptr and
- * kv_last_page_len and writes the split-K work list into `workspace`; it does
- * not touch the host.  mi_decode_run reads only the work list, so one plan
- * serves every layer of a step and a graph-captured run replays correctly
- * after any later plan with the same (batch_size, heads, head_dim) shape.
+ * mi_decode_plan runs a one-workgroup GPU kernel that reads kv_indptr,
+ * kv_last_page_len and the first page ids of each split from kv_indices, and
+ * writes the split-K work list into `workspace`; it does not touch the host.
+ * mi_decode_run reads the work list and kv_indices (which must not change
+ * between plan and run), so one plan serves every layer of a step and a
+ * graph-captured run replays correctly after any later plan with the same
+ * (batch_size, heads, head_dim) shape.
  *
  * q / out: [batch][num_qo_heads][head_dim] bf16 (element strides given).
  * Q head h reads KV head h / (num_qo_heads / num_kv_heads): any integer group
  * size 1..8 runs natively (no head padding).  sm_scale <= 0 selects
  * 1/sqrt(head_dim).  head_dim in {64, 128, 256}; page_size == 16.
+ * max_units <= 0 lets plan and run size the work list from workspace_bytes
+ * (both must then see the same workspace_bytes); mi_decode_workspace_size
+ * with max_units <= 0 returns a size suited to 8 units per compute unit.
  * ------------------------------------------------------------------------ */
 size_t mi_decode_workspace_size(int32_t batch_size, int32_t num_qo_heads, int32_t num_kv_heads,
                                 int32_t head_dim, int32_t max_units);
 
 int mi_decode_plan(void* workspace, size_t workspace_bytes, const int32_t* kv_indptr,
-                   const int32_t* kv_last_page_len, int32_t batch_size, int32_t num_qo_heads,
-                   int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int32_t max_units,
-                   mi_stream_t stream);
+                   const int32_t* kv_indices, const int32_t* kv_last_page_len, int32_t batch_size,
+                   int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                   int32_t max_units, mi_stream_t stream);
 
 int mi_decode_run(void* workspace, size_t workspace_bytes, const void* q, int64_t q_stride_batch,
                   int64_t q_stride_head, const void* paged_kv_cache, int64_t num_pages,

@@ -41,7 +41,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mi_decode_workspace_size": (_c_sz, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "mi_decode_plan": (
         ctypes.c_int,
-        [_vp, _c_sz, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp],
+        [_vp, _c_sz, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp],
     ),
     "mi_decode_run": (
         ctypes.c_int,

@@ -7,22 +7,30 @@
 //
 // Work decomposition.  plan() cuts every request's page list into `nsplit`
 // contiguous page ranges ("items") so that items x kv_heads ("units") is close
-// to 8 units per CU.  One 64-lane wave runs one unit: it streams the unit's K
+// to kUnitsPerCU units per CU, and copies the first kInlinePages page ids of
+// each item into the item so a wave can start its page loads right after
+// reading the item.  One 64-lane wave runs one unit: it streams the unit's K
 // and V pages for one KV head and serves all `group` Q heads of that KV head,
 // so each KV byte is read from HBM once per step.
 //
 // Per 16-token page, one wave:
-//   * S = Q K^T with four 16x16x32 bf16 MFMAs (head_dim 128): Q rows are the
-//     group's heads (zero-padded to 16), K columns are the page's tokens, and
-//     each lane's 16-byte global load of K is directly its B operand;
+//   * S = Q K^T with 16x16x32 bf16 MFMAs: Q rows are the group's heads
+//     (zero-padded to 16), K columns are the page's tokens, and each lane's
+//     16-byte global load of K is directly its B operand;
 //   * online softmax in the exp2 domain with a lazy running max (rescale only
 //     when the max grows by more than 2^8, so rescales are rare);
-//   * O += P V on the VALU: lane (t, c) holds 8..32 head_dim values of token t
+//   * O += P V on the VALU: lane (t, c) holds 16 head_dim values of token t
 //     and accumulates them for all group heads; P reaches it by ds_bpermute.
-// At the end the per-token partial sums are reduced through LDS.  Units of a
-// request with several splits write (O, m, l) partials; the last unit to
-// finish (device-scope counter) merges them and resets the counter, so run()
-// is a single launch and needs no memset.
+// Pages are triple-buffered in registers (two pages in flight while one is
+// consumed).  At the end the per-token partial sums are reduced through LDS.
+//
+// Split merge without cache flushes.  Units of a request with several splits
+// write (O, m, l) partials with device-coherent (sc1, write-through) stores,
+// wait for them, and bump a per-(request, KV head) counter; the unit that
+// sees the count reach nsplit-1 reads the partials back with device-coherent
+// loads, merges them, and resets the counter.  No agent-scope fence (and so
+// no whole-L2 writeback / invalidate) is executed, and run() is one launch
+// with no memset.
 #include <math.h>
 
 #include "mi_common.h"
@@ -31,10 +39,15 @@ namespace {
 
 constexpr int kPageSize = 16;
 constexpr float kLazyRescale = 8.0f;  // log2 units
-constexpr int kMaxSplits = 64;        // splits per request (one lane each in the merge)
-constexpr int kUnitsPerCU = 8;
+#ifndef MI_DECODE_UNITS_PER_CU
+#define MI_DECODE_UNITS_PER_CU 8
+#endif
+constexpr int kUnitsPerCU = MI_DECODE_UNITS_PER_CU;
+constexpr int kInlinePages = 8;
+// s_waitcnt immediate (gfx9 encoding): vmcnt = 0, expcnt = 7, lgkmcnt = 15.
+constexpr int kWaitVmcnt0 = 0x0F70;
 
-struct alignas(32) DecodeItem {
+struct alignas(64) DecodeItem {
   int b;           // request
   int page_begin;  // absolute position in kv_indices
   int page_end;
@@ -43,6 +56,7 @@ struct alignas(32) DecodeItem {
   int nsplit;
   int item_base;  // item index of split 0 of this request
   int pad;
+  int pages[kInlinePages];  // kv_indices[page_begin ..] copied by plan()
 };
 
 struct DecodeHeader {
@@ -74,13 +88,25 @@ DecodeLayout decode_layout(int batch, int hq, int hkv, int head_dim, int max_uni
   return L;
 }
 
-int default_max_units(int batch, int hkv) {
-  return 2 * mi::num_cus() * kUnitsPerCU + batch * hkv;
+// Units the workspace holds when the caller does not fix max_units: all of
+// it, capped at 65536 (enough for 8-page items over ~32M tokens x heads).
+int units_that_fit(size_t bytes, int batch, int hq, int hkv, int head_dim) {
+  const int group = hq / hkv;
+  const size_t fixed = 256 + 2 * 256 + size_t(batch) * hkv * sizeof(int);
+  if (bytes <= fixed) return 0;
+  const size_t per_unit = sizeof(DecodeItem) / size_t(hkv) + 1 + size_t(group) * (2 + head_dim) * sizeof(float);
+  size_t n = (bytes - fixed) / per_unit;
+  n = n > 65536 ? 65536 : n;
+  while (n > 0 && decode_layout(batch, hq, hkv, head_dim, int(n)).total > bytes) n -= hkv;
+  return int(n);
 }
+
+int default_max_units(int batch, int hkv) { return 4 * mi::num_cus() * kUnitsPerCU + batch * hkv; }
 
 // ------------------------------------------------------------------ plan
 struct PlanParams {
   const int32_t* indptr;
+  const int32_t* indices;
   const int32_t* last_page_len;
   int batch, hkv, target_units, max_items;
   DecodeHeader* header;
@@ -143,12 +169,11 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
   }
   const int total_pages = block_sum(tot, red);
   const int max_np = block_max(mx, red);
-  // Pages per item: aim at target_units units, never more than kMaxSplits
-  // splits per request, never more items than the workspace holds.
-  long long want = (long long)total_pages * p.hkv;
+  // Pages per item: aim at target_units units with at most kInlinePages
+  // pages per item; grow only if the workspace cannot hold that many items.
+  const long long want = (long long)total_pages * p.hkv;
   int chunk = int((want + p.target_units - 1) / p.target_units);
-  chunk = max(chunk, 1);
-  chunk = max(chunk, (max_np + kMaxSplits - 1) / kMaxSplits);
+  chunk = min(max(chunk, 1), kInlinePages);
   for (;;) {
     int cnt = 0;
     for (int b = t; b < p.batch; b += blockDim.x) {
@@ -184,6 +209,8 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
         it.nsplit = ns;
         it.item_base = first;
         it.pad = 0;
+        for (int j = 0; j < kInlinePages; ++j)
+          it.pages[j] = (it.page_begin + j < it.page_end) ? p.indices[it.page_begin + j] : -1;
         p.items[first + s] = it;
       }
     }
@@ -202,13 +229,14 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
 // ------------------------------------------------------------------ run
 template <int D, int G>
 struct DecodeTraits {
-  static constexpr int KSTEPS = D / 32;                       // MFMA k-steps for q.k
-  static constexpr int DL = (G <= 4 && D >= 128) ? 32 : 16;  // head_dim values per lane in P.V
-  static constexpr int LPT = D / DL;                          // lanes per token row
-  static constexpr int TPP = 64 / LPT;                        // tokens per pass
+  static constexpr int KSTEPS = D / 32;  // MFMA k-steps for q.k
+  static constexpr int DL = 16;          // head_dim values per lane in P.V
+  static constexpr int LPT = D / DL;     // lanes per token row
+  static constexpr int TPP = 64 / LPT;   // tokens per pass
   static constexpr int PASSES = kPageSize / TPP;
   static constexpr int VL = DL / 8;   // 16-byte V loads per pass
   static constexpr int OUT = D / 64;  // reduced outputs per head per lane
+  static constexpr int NBUF = (D <= 128) ? 3 : 2;  // pages held in registers
   static_assert(TPP <= kPageSize && kPageSize % TPP == 0, "pass geometry");
   static_assert(G >= 1 && G <= 8, "group size");
 };
@@ -231,20 +259,57 @@ struct RunParams {
 };
 
 template <int D, int G>
+struct PageRegs {
+  uint4 k[DecodeTraits<D, G>::KSTEPS];
+  uint4 v[DecodeTraits<D, G>::PASSES][DecodeTraits<D, G>::VL];
+};
+
+template <typename F>
+__device__ __forceinline__ F coherent_load(const F* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename F>
+__device__ __forceinline__ void coherent_store(F* p, F v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int D, int G>
 __device__ __forceinline__ void decode_unit(const RunParams& p, int u, float (*red)[D + 4]) {
   using T = DecodeTraits<D, G>;
+  using Regs = PageRegs<D, G>;
   const int lane = threadIdx.x;
   const int item_idx = u / p.hkv;
   const int hkv = u - item_idx * p.hkv;
-  const DecodeItem it = p.items[item_idx];
-  const int b = it.b;
+  const DecodeItem& itr = p.items[item_idx];
+  const int b = itr.b;
+  const int page_begin = itr.page_begin, page_end = itr.page_end, last_valid = itr.last_valid;
+  const int nsplit = itr.nsplit, item_base = itr.item_base;
+  const int npg = page_end - page_begin;
 
   const int64_t tok_stride = int64_t(p.hkv) * D;
   const int64_t kv_stride = kPageSize * tok_stride;
   const int64_t page_stride = 2 * kv_stride;
 
-  // Q as the A operand: row m = head within the group.
   const int m = lane & 15, kb = lane >> 4;
+  const int tv = lane % T::TPP, cv = lane / T::TPP;
+  const int64_t k_off = int64_t(m) * tok_stride + int64_t(hkv) * D + kb * 8;
+  const int64_t v_off = kv_stride + int64_t(tv) * tok_stride + int64_t(hkv) * D + cv * 8;
+
+  // Loads are unconditional so the compiler can keep them in flight across
+  // the page loop: an invalid page id reads page 0 and is masked in consume.
+  auto load_page = [&](Regs& r, int page) {
+    const int safe = (page >= 0 && page < p.num_pages) ? page : 0;
+    const uint16_t* pg = p.pool + int64_t(safe) * page_stride;
+#pragma unroll
+    for (int s = 0; s < T::KSTEPS; ++s) r.k[s] = mi::load16(pg + k_off + s * 32);
+#pragma unroll
+    for (int ps = 0; ps < T::PASSES; ++ps)
+#pragma unroll
+      for (int j = 0; j < T::VL; ++j)
+        r.v[ps][j] = mi::load16(pg + v_off + int64_t(ps * T::TPP) * tok_stride + j * (T::LPT * 8));
+  };
+
+  // Q as the A operand: row m = head within the group.
   mi::bf16x8_t qa[T::KSTEPS];
   {
     const uint16_t* qrow = p.q + int64_t(b) * p.q_sb + int64_t(hkv * G + (m < G ? m : 0)) * p.q_sh + kb * 8;
@@ -255,9 +320,6 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, float (*r
       qa[s] = mi::as_bf16x8(v);
     }
   }
-  const int tv = lane % T::TPP, cv = lane / T::TPP;
-  const int64_t k_off = int64_t(m) * tok_stride + int64_t(hkv) * D + kb * 8;
-  const int64_t v_off = kv_stride + int64_t(tv) * tok_stride + int64_t(hkv) * D + cv * 8;
 
   float acc[G][T::DL];
 #pragma unroll
@@ -270,106 +332,95 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, float (*r
   float lrow[4] = {0.f, 0.f, 0.f, 0.f};
   const int row = lane >> 4;  // S-layout row group: heads 4*row .. 4*row+3
 
-  for (int base = it.page_begin; base < it.page_end; base += 64) {
-    const int nblk = min(64, it.page_end - base);
-    const int pid = (lane < nblk) ? p.indices[base + lane] : 0;
-    uint4 kn[T::KSTEPS], vn[T::PASSES][T::VL];
-    auto load_page = [&](int page) {
-      if (page < 0 || page >= p.num_pages) {  // invalid page id: read nothing, contribute zeros
+  // valid: tokens of the page that take part (0 for an invalid page id)
+  auto consume = [&](const Regs& r, int valid) {
+    // ---- S = Q K^T (lane: heads 4*row+i, token lane&15)
+    mi::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < T::KSTEPS; ++s) kn[s] = make_uint4(0, 0, 0, 0);
+    for (int s = 0; s < T::KSTEPS; ++s) c = mi::mfma_16x16x32_bf16(qa[s], mi::as_bf16x8(r.k[s]), c);
+    const int tok = lane & 15;
+    float s2[4];
 #pragma unroll
-        for (int ps = 0; ps < T::PASSES; ++ps)
-#pragma unroll
-          for (int j = 0; j < T::VL; ++j) vn[ps][j] = make_uint4(0, 0, 0, 0);
-        return;
-      }
-      const uint16_t* pg = p.pool + int64_t(page) * page_stride;
-#pragma unroll
-      for (int s = 0; s < T::KSTEPS; ++s) kn[s] = mi::load16(pg + k_off + s * 32);
-#pragma unroll
-      for (int ps = 0; ps < T::PASSES; ++ps)
-#pragma unroll
-        for (int j = 0; j < T::VL; ++j)
-          vn[ps][j] = mi::load16(pg + v_off + int64_t(ps * T::TPP) * tok_stride + j * (T::LPT * 8));
-    };
-    load_page(mi::read_lane_i(pid, 0));
-    for (int k = 0; k < nblk; ++k) {
-      uint4 kc[T::KSTEPS], vc[T::PASSES][T::VL];
-#pragma unroll
-      for (int s = 0; s < T::KSTEPS; ++s) kc[s] = kn[s];
-#pragma unroll
-      for (int ps = 0; ps < T::PASSES; ++ps)
-#pragma unroll
-        for (int j = 0; j < T::VL; ++j) vc[ps][j] = vn[ps][j];
-      if (k + 1 < nblk) load_page(mi::read_lane_i(pid, k + 1));
-      const int valid = (base + k == it.page_end - 1) ? it.last_valid : kPageSize;
+    for (int i = 0; i < 4; ++i) s2[i] = (tok < valid) ? c[i] * p.scale_log2 : -INFINITY;
 
-      // ---- S = Q K^T (lane: heads 4*row+i, token lane&15)
-      mi::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+    // ---- page max per head, lazy rescale
+    float rm[4];
 #pragma unroll
-      for (int s = 0; s < T::KSTEPS; ++s) c = mi::mfma_16x16x32_bf16(qa[s], mi::as_bf16x8(kc[s]), c);
-      const int tok = lane & 15;
-      float s2[4];
+    for (int i = 0; i < 4; ++i) rm[i] = mi::group16_max(s2[i]);
+    float mp[G];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s2[i] = (tok < valid) ? c[i] * p.scale_log2 : -INFINITY;
-
-      // ---- page max per head, lazy rescale
-      float rm[4];
+    for (int h = 0; h < G; ++h) mp[h] = mi::read_lane(rm[h & 3], (h >> 2) * 16);
+    bool need = false;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) rm[i] = mi::group16_max(s2[i]);
-      float mp[G];
+    for (int h = 0; h < G; ++h) need |= (mp[h] > mh[h] + kLazyRescale);
+    if (need) {
+      float f[8];
 #pragma unroll
-      for (int h = 0; h < G; ++h) mp[h] = mi::read_lane(rm[h & 3], (h >> 2) * 16);
-      bool need = false;
+      for (int h = 0; h < 8; ++h) f[h] = 1.f;
 #pragma unroll
-      for (int h = 0; h < G; ++h) need |= (mp[h] > mh[h] + kLazyRescale);
-      if (need) {
-        float f[8];
+      for (int h = 0; h < G; ++h) {
+        if (mp[h] > mh[h] + kLazyRescale) {
+          f[h] = (mh[h] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mh[h] - mp[h]);
+          mh[h] = mp[h];
 #pragma unroll
-        for (int h = 0; h < 8; ++h) f[h] = 1.f;
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-          if (mp[h] > mh[h] + kLazyRescale) {
-            f[h] = (mh[h] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mh[h] - mp[h]);
-            mh[h] = mp[h];
-#pragma unroll
-            for (int j = 0; j < T::DL; ++j) acc[h][j] *= f[h];
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) lrow[i] *= (row == 0) ? f[i] : f[4 + i];
-      }
-      float pS[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float mm = 0.f;
-        if (i < G) mm = mh[i];
-        if (row == 1 && 4 + i < G) mm = mh[(4 + i < G) ? 4 + i : 0];
-        pS[i] = __builtin_amdgcn_exp2f(s2[i] - mm);
-        lrow[i] += pS[i];
-      }
-
-      // ---- O += P V
-#pragma unroll
-      for (int ps = 0; ps < T::PASSES; ++ps) {
-        const int tsrc = tv + ps * T::TPP;
-        float pv[G];
-#pragma unroll
-        for (int h = 0; h < G; ++h) pv[h] = mi::lane_shuffle(pS[h & 3], (h >> 2) * 16 + tsrc);
-        const bool vmask = tsrc >= valid;
-#pragma unroll
-        for (int j = 0; j < T::VL; ++j) {
-          uint4 v = vc[ps][j];
-          if (vmask) v = make_uint4(0, 0, 0, 0);
-          float vf[8] = {mi::bf16_lo(v.x), mi::bf16_hi(v.x), mi::bf16_lo(v.y), mi::bf16_hi(v.y),
-                         mi::bf16_lo(v.z), mi::bf16_hi(v.z), mi::bf16_lo(v.w), mi::bf16_hi(v.w)};
-#pragma unroll
-          for (int h = 0; h < G; ++h)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][j * 8 + e] = fmaf(pv[h], vf[e], acc[h][j * 8 + e]);
+          for (int j = 0; j < T::DL; ++j) acc[h][j] *= f[h];
         }
       }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lrow[i] *= (row == 0) ? f[i] : f[4 + i];
+    }
+    float pS[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float mm = 0.f;
+      if (i < G) mm = mh[i];
+      if (row == 1 && 4 + i < G) mm = mh[(4 + i < G) ? 4 + i : 0];
+      pS[i] = (s2[i] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(s2[i] - mm);
+      lrow[i] += pS[i];
+    }
+
+    // ---- O += P V
+#pragma unroll
+    for (int ps = 0; ps < T::PASSES; ++ps) {
+      const int tsrc = tv + ps * T::TPP;
+      float pv[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) pv[h] = mi::lane_shuffle(pS[h & 3], (h >> 2) * 16 + tsrc);
+      const bool vmask = tsrc >= valid;
+#pragma unroll
+      for (int j = 0; j < T::VL; ++j) {
+        uint4 v = r.v[ps][j];
+        if (vmask) v = make_uint4(0, 0, 0, 0);
+        const float vf[8] = {mi::bf16_lo(v.x), mi::bf16_hi(v.x), mi::bf16_lo(v.y), mi::bf16_hi(v.y),
+                             mi::bf16_lo(v.z), mi::bf16_hi(v.z), mi::bf16_lo(v.w), mi::bf16_hi(v.w)};
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[h][j * 8 + e] = fmaf(pv[h], vf[e], acc[h][j * 8 + e]);
+      }
+    }
+  };
+
+  // ---- stream the pages in groups of kInlinePages.  Lane j of `pid` holds
+  // the group's j-th page id (the item's inline copy for group 0), read once
+  // per group; v_readlane then yields wave-uniform ids without further memory
+  // waits.  Inside a group the loop is unrolled so NBUF-1 pages are in
+  // flight while one is consumed.
+  for (int g0 = 0; g0 < npg; g0 += kInlinePages) {
+    const int cnt = min(kInlinePages, npg - g0);
+    int pid = -1;
+    if (lane < cnt) pid = (g0 == 0) ? itr.pages[lane] : p.indices[page_begin + g0 + lane];
+    Regs buf[T::NBUF];
+#pragma unroll
+    for (int i = 0; i < T::NBUF - 1; ++i) load_page(buf[i], mi::read_lane_i(pid, min(i, cnt - 1)));
+#pragma unroll
+    for (int i = 0; i < kInlinePages; ++i) {
+      if (i >= cnt) break;
+      load_page(buf[(i + T::NBUF - 1) % T::NBUF], mi::read_lane_i(pid, min(i + T::NBUF - 1, cnt - 1)));
+      const int page = mi::read_lane_i(pid, i);
+      int valid = (g0 + i == npg - 1) ? last_valid : kPageSize;
+      if (page < 0 || page >= p.num_pages) valid = 0;
+      consume(buf[i % T::NBUF], valid);
     }
   }
 
@@ -406,7 +457,7 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, float (*r
     __syncthreads();
   }
 
-  if (it.nsplit == 1) {
+  if (nsplit == 1) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       const float inv = lh[h] > 0.f ? 1.f / lh[h] : 0.f;
@@ -417,13 +468,13 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, float (*r
     return;
   }
 
-  // ---- split-K: publish the partial, the last unit of (b, hkv) merges.
+  // ---- split-K: publish the partial (write-through), count, last unit merges
   {
     float* po = p.po + int64_t(u) * G * D;
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
-      for (int k = 0; k < T::OUT; ++k) po[h * D + lane + 64 * k] = o[h][k];
+      for (int k = 0; k < T::OUT; ++k) coherent_store(po + h * D + lane + 64 * k, o[h][k]);
     if (lane < G) {
       float mv = 0.f, lv = 0.f;
 #pragma unroll
@@ -432,50 +483,87 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, float (*r
           mv = mh[h];
           lv = lh[h];
         }
-      p.pml[(int64_t(u) * G + lane) * 2 + 0] = mv;
-      p.pml[(int64_t(u) * G + lane) * 2 + 1] = lv;
+      coherent_store(p.pml + (int64_t(u) * G + lane) * 2 + 0, mv);
+      coherent_store(p.pml + (int64_t(u) * G + lane) * 2 + 1, lv);
     }
   }
-  __threadfence();
+  // Wait until this wave's write-through stores are acknowledged (vmcnt 0;
+  // expcnt / lgkmcnt left free), so they are visible device-wide before the
+  // counter moves.  The fence keeps the compiler from reordering around it.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   int prev = 0;
   int* counter = p.counters + b * p.hkv + hkv;
-  if (lane == 0)
-    prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0) prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   prev = mi::read_lane_i(prev, 0);
-  if (prev != it.nsplit - 1) return;
-  __threadfence();
+  if (prev != nsplit - 1) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 
-  const int ns = it.nsplit;
-  const int my_unit = (it.item_base + lane) * p.hkv + hkv;  // split `lane`
+  // Online merge over the splits, 64 per round (lane s holds split s's m, l).
+  float M[G], Lt[G], sum[G][T::OUT];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    float ms = -INFINITY, ls = 0.f;
-    if (lane < ns) {
-      ms = __hip_atomic_load(p.pml + (int64_t(my_unit) * G + h) * 2 + 0, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-      ls = __hip_atomic_load(p.pml + (int64_t(my_unit) * G + h) * 2 + 1, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-    }
-    const float M = mi::wave_max(ms);
-    const float w = (lane < ns) ? __builtin_amdgcn_exp2f(ms - M) : 0.f;
-    const float Lt = mi::wave_sum(w * ls);
-    const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
-    float sum[T::OUT];
+    M[h] = -INFINITY;
+    Lt[h] = 0.f;
 #pragma unroll
-    for (int k = 0; k < T::OUT; ++k) sum[k] = 0.f;
-    for (int s = 0; s < ns; ++s) {
-      const float ws = mi::read_lane(w, s);
-      const int us = (it.item_base + s) * p.hkv + hkv;
-      const float* src = p.po + (int64_t(us) * G + h) * D;
+    for (int k = 0; k < T::OUT; ++k) sum[h][k] = 0.f;
+  }
+  for (int r0 = 0; r0 < nsplit; r0 += 64) {
+    const int nr = min(64, nsplit - r0);
+    const int my_unit = (item_base + r0 + lane) * p.hkv + hkv;
+    float ms[G], ls[G], wgt[G];
 #pragma unroll
-      for (int k = 0; k < T::OUT; ++k)
-        sum[k] += ws * __hip_atomic_load(src + lane + 64 * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int h = 0; h < G; ++h) {
+      ms[h] = -INFINITY;
+      ls[h] = 0.f;
+      if (lane < nr) {
+        ms[h] = coherent_load(p.pml + (int64_t(my_unit) * G + h) * 2 + 0);
+        ls[h] = coherent_load(p.pml + (int64_t(my_unit) * G + h) * 2 + 1);
+      }
     }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float Mn = fmaxf(M[h], mi::wave_max(ms[h]));
+      const float f = (M[h] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M[h] - Mn);
+      Lt[h] *= f;
+#pragma unroll
+      for (int k = 0; k < T::OUT; ++k) sum[h][k] *= f;
+      wgt[h] = (lane < nr && ms[h] != -INFINITY) ? __builtin_amdgcn_exp2f(ms[h] - Mn) : 0.f;
+      Lt[h] += mi::wave_sum(wgt[h] * ls[h]);
+      M[h] = Mn;
+    }
+    constexpr int kBatch = 4;  // splits whose partials are in flight together
+    for (int s0 = 0; s0 < nr; s0 += kBatch) {
+      float v[kBatch][G][T::OUT];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int s = r0 + min(s0 + j, nr - 1);
+        const float* src = p.po + int64_t((item_base + s) * p.hkv + hkv) * G * D;
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+          for (int k = 0; k < T::OUT; ++k) v[j][h][k] = coherent_load(src + h * D + lane + 64 * k);
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        if (s0 + j >= nr) break;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          const float ws = mi::read_lane(wgt[h], s0 + j);
+#pragma unroll
+          for (int k = 0; k < T::OUT; ++k) sum[h][k] += ws * v[j][h][k];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const float inv = Lt[h] > 0.f ? 1.f / Lt[h] : 0.f;
     uint16_t* orow = p.out + int64_t(b) * p.o_sb + int64_t(hkv * G + h) * p.o_sh;
 #pragma unroll
-    for (int k = 0; k < T::OUT; ++k) orow[lane + 64 * k] = mi::f32_to_bf16(sum[k] * inv);
+    for (int k = 0; k < T::OUT; ++k) orow[lane + 64 * k] = mi::f32_to_bf16(sum[h][k] * inv);
   }
-  if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0) coherent_store(counter, 0);
 }
 
 template <int D, int G>
@@ -534,24 +622,25 @@ extern "C" size_t mi_decode_workspace_size(int32_t batch_size, int32_t num_qo_he
 }
 
 extern "C" int mi_decode_plan(void* workspace, size_t workspace_bytes, const int32_t* kv_indptr,
-                              const int32_t* kv_last_page_len, int32_t batch_size,
-                              int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
-                              int32_t page_size, int32_t max_units, mi_stream_t stream) {
+                              const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                              int32_t batch_size, int32_t num_qo_heads, int32_t num_kv_heads,
+                              int32_t head_dim, int32_t page_size, int32_t max_units, mi_stream_t stream) {
   mi::clear_error();
   int rc = check_shape("decode plan", batch_size, num_qo_heads, num_kv_heads, head_dim, page_size);
   if (rc) return rc;
-  if (max_units <= 0) max_units = default_max_units(batch_size, num_kv_heads);
+  if (max_units <= 0) max_units = units_that_fit(workspace_bytes, batch_size, num_qo_heads, num_kv_heads, head_dim);
   const DecodeLayout L = decode_layout(batch_size, num_qo_heads, num_kv_heads, head_dim, max_units);
   if (!workspace || workspace_bytes < L.total)
     return mi::fail(MI_ERR_WORKSPACE, "decode plan: workspace %zu bytes, need %zu", workspace_bytes, L.total);
   if (L.max_items < batch_size)
-    return mi::fail(MI_ERR_INVALID, "decode plan: max_units %d below batch*kv_heads %d", max_units,
-                    batch_size * num_kv_heads);
-  if (batch_size > 0 && (!kv_indptr || !kv_last_page_len))
-    return mi::fail(MI_ERR_INVALID, "decode plan: null indptr / last_page_len");
+    return mi::fail(MI_ERR_WORKSPACE, "decode plan: room for %d units, need at least batch*kv_heads = %d",
+                    max_units, batch_size * num_kv_heads);
+  if (batch_size > 0 && (!kv_indptr || !kv_indices || !kv_last_page_len))
+    return mi::fail(MI_ERR_INVALID, "decode plan: null indptr / indices / last_page_len");
   char* ws = static_cast<char*>(workspace);
   PlanParams pp;
   pp.indptr = kv_indptr;
+  pp.indices = kv_indices;
   pp.last_page_len = kv_last_page_len;
   pp.batch = batch_size;
   pp.hkv = num_kv_heads;
@@ -574,7 +663,7 @@ extern "C" int mi_decode_run(void* workspace, size_t workspace_bytes, const void
   int rc = check_shape("decode run", batch_size, num_qo_heads, num_kv_heads, head_dim, page_size);
   if (rc) return rc;
   if (batch_size == 0) return MI_OK;
-  if (max_units <= 0) max_units = default_max_units(batch_size, num_kv_heads);
+  if (max_units <= 0) max_units = units_that_fit(workspace_bytes, batch_size, num_qo_heads, num_kv_heads, head_dim);
   const DecodeLayout L = decode_layout(batch_size, num_qo_heads, num_kv_heads, head_dim, max_units);
   if (!workspace || workspace_bytes < L.total)
     return mi::fail(MI_ERR_WORKSPACE, "decode run: workspace %zu bytes, need %zu", workspace_bytes, L.total);

@@ -13,9 +13,11 @@ Differences that matter to a caller:
     Q heads to a power-of-two group (model.py:134-137, 226-243) is not needed.
   * ``run`` reads the work list ``plan`` left in the workspace and the page
     ids from the ``indices`` tensor given to ``plan`` (kept by reference, as
-    the reference relies on, scheduler.py:898-899); its grid is fixed per
-    (batch, heads, head_dim), so a graph captured once replays correctly
-    after every later ``plan``.
+    the reference relies on, scheduler.py:898-899); ``plan`` also copies the
+    first page ids of each split into the work list, so ``indices`` must not
+    change between ``plan`` and ``run`` (the reference never does that).  The
+    grid of ``run`` is fixed per (batch, heads, head_dim), so a graph captured
+    once replays correctly after every later ``plan``.
 """
 
 from __future__ import annotations
@@ -75,7 +77,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
             raise ValueError(f"num_qo_heads {num_qo_heads} is not a multiple of num_kv_heads {num_kv_heads}")
         _lib.call(
             "mi_decode_plan", self._ws.data_ptr(), self._ws_bytes, indptr.data_ptr(),
-            last_page_len.data_ptr(), batch, num_qo_heads, num_kv_heads, head_dim, page_size, 0,
+            indices.data_ptr(), last_page_len.data_ptr(), batch, num_qo_heads, num_kv_heads, head_dim, page_size, 0,
             stream_of(indptr),
         )
         self._batch = batch

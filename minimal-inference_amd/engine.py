@@ -1,0 +1,303 @@
+"""Continuous-batching driver over the paged-attention path.
+
+Restates the reference scheduler's semantics (scheduler.py:477-1009) on top
+of the device page table and the HIP kernels:
+
+* step order admit -> prefill -> decode -> retire (scheduler.py:596-600);
+* admission in FIFO order while the batch has room, stopping at the first
+  request whose ceil(len / page_size) pages do not fit (624-637);
+* decode growth before the step's metadata, in active order (843-847);
+* retirement at the end of the step releases pages in active order
+  (984-1003); released pages are zeroed in every layer (216-221);
+* greedy rows (temperature <= 0) take argmax, others sample (319-343).
+
+What changes (the north star's items):
+* page lists, the free-page ring and the CSR / padding metadata live on the
+  GPU (``DevicePageTable``); the host keeps counts only;
+* all requests admitted in a step are prefilled in one ragged batch (the
+  reference prefills one request per forward, scheduler.py:643-652);
+* the decode forward *and* the sampler are captured in one hipGraph per
+  padded batch size; ``plan()`` runs outside the graph each step; padded rows
+  own the scratch page, so their K/V appends land there by construction.
+
+Per decode step the host performs one small host->device copy of op lists and
+input ids, launches the page-table kernel, ``plan()`` and the graph, and
+waits once for the sampled ids (needed to stream tokens and detect EOS).
+"""
+
+from __future__ import annotations
+
+import enum
+import math
+import time
+from collections import deque
+from dataclasses import dataclass, field
+
+import torch
+
+from .decode import BatchDecodeWithPagedKVCacheWrapper
+from .kv_cache import DevicePageTable, PagedKVCache
+from .model import AttentionBackend, Model
+from .prefill import BatchPrefillWithPagedKVCacheWrapper
+from .sampling import Sampler
+
+GRAPH_BATCH_SIZES = [1, 2, 4, 8, 16, 32, 48, 64]  # scheduler.py:350
+
+
+class RequestStatus(enum.Enum):
+    WAITING = "waiting"
+    PREFILLING = "prefilling"
+    DECODING = "decoding"
+    FINISHED = "finished"
+
+
+@dataclass
+class Request:
+    request_id: str
+    input_ids: list[int]
+    max_new_tokens: int
+    temperature: float = 0.0
+    top_p: float = 1.0
+    status: RequestStatus = RequestStatus.WAITING
+    generated_tokens: list[int] = field(default_factory=list)
+    current_position: int = 0
+    slot: int = -1
+    finish_reason: str | None = None
+    prefill_done_time: float = 0.0
+    last_token_time: float = 0.0
+
+
+class _Pinned:
+    """Pinned host staging buffer with an event guarding its last copy."""
+
+    def __init__(self, n: int, dtype):
+        self.buf = torch.zeros(n, dtype=dtype).pin_memory()
+        self.evt: torch.cuda.Event | None = None
+
+    def upload(self, values, dst: torch.Tensor) -> None:
+        if self.evt is not None:
+            self.evt.synchronize()
+        n = len(values)
+        self.buf[:n] = torch.as_tensor(values, dtype=self.buf.dtype)
+        dst[:n].copy_(self.buf[:n], non_blocking=True)
+        self.evt = torch.cuda.Event()
+        self.evt.record()
+
+
+class Scheduler:
+    def __init__(self, model: Model, max_batch_size: int = 8, max_seq_len: int = 4096, page_size: int = 16,
+                 num_pages: int | None = None, eos_token_ids: set[int] | None = None, use_graphs: bool = True,
+                 seed: int = 0, workspace_mb: int = 128, zero_released_pages: bool = True):
+        cfg = model.cfg
+        self.model = model
+        self.device = model.device
+        self.page_size = page_size
+        self.max_batch_size = max_batch_size
+        self.max_seq_len = max_seq_len
+        self.eos = set(eos_token_ids or ())
+        self.zero_released = zero_released_pages
+        self.kv = PagedKVCache(cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim, max_batch_size,
+                               max_seq_len, page_size, self.device, max_num_pages=num_pages)
+        mpps = math.ceil(max_seq_len / page_size) + 1
+        self.pt = DevicePageTable(self.kv.max_num_pages, max_batch_size, mpps, page_size, self.device)
+        dev = self.device
+        ws = workspace_mb << 20
+        self.decode_wrapper = BatchDecodeWithPagedKVCacheWrapper(torch.empty(ws, dtype=torch.uint8, device=dev))
+        self.prefill_wrapper = BatchPrefillWithPagedKVCacheWrapper(torch.empty(ws, dtype=torch.uint8, device=dev))
+        self.graph_sizes = [b for b in GRAPH_BATCH_SIZES if b < max_batch_size] + [max_batch_size]
+        bmax = self.graph_sizes[-1]
+        cap = bmax * mpps + bmax
+        # static decode buffers (shared by every captured graph)
+        self.d_indptr = torch.zeros(bmax + 1, dtype=torch.int32, device=dev)
+        self.d_indices = torch.full((cap,), self.kv.scratch_page, dtype=torch.int32, device=dev)
+        self.d_last = torch.ones(bmax, dtype=torch.int32, device=dev)
+        self.d_batch = torch.arange(bmax, dtype=torch.int32, device=dev)
+        self.d_pos = torch.zeros(bmax, dtype=torch.int32, device=dev)
+        self.d_ids = torch.zeros(bmax, dtype=torch.int64, device=dev)
+        self.sampler = Sampler(dev, bmax, seed=seed)
+        # prefill buffers
+        self.p_indptr = torch.zeros(max_batch_size + 1, dtype=torch.int32, device=dev)
+        self.p_indices = torch.zeros(max_batch_size * mpps, dtype=torch.int32, device=dev)
+        self.p_last = torch.ones(max_batch_size, dtype=torch.int32, device=dev)
+        self.p_batch_dummy = torch.zeros(max_batch_size, dtype=torch.int32, device=dev)
+        self.p_pos_dummy = torch.zeros(max_batch_size, dtype=torch.int32, device=dev)
+        self.p_sampler = Sampler(dev, max_batch_size, seed=seed + 1)
+        self._up_ids = _Pinned(bmax, torch.int64)
+        self._up_t = _Pinned(bmax, torch.float32)
+        self._up_p = _Pinned(bmax, torch.float32)
+        self._tok_host = torch.zeros(max(bmax, max_batch_size), dtype=torch.int64).pin_memory()
+        self.waiting: deque[Request] = deque()
+        self.active: list[Request] = []
+        self.free_slots: deque[int] = deque(range(max_batch_size))
+        self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
+        self.steps = 0
+        if use_graphs:
+            self._capture_graphs()
+
+    # ------------------------------------------------------------------ API
+    def submit(self, req: Request) -> None:
+        self.waiting.append(req)
+
+    def has_work(self) -> bool:
+        return bool(self.waiting or self.active)
+
+    def run(self, max_steps: int | None = None) -> None:
+        n = 0
+        while self.has_work() and (max_steps is None or n < max_steps):
+            self.step()
+            n += 1
+
+    # ------------------------------------------------------------------ graphs
+    def _backend(self, wrapper, mode, indptr, indices, last, batch, pos):
+        return AttentionBackend(self.kv, wrapper, mode, indptr, indices, last, None, batch, pos)
+
+    def _decode_forward(self, bs: int) -> torch.Tensor:
+        be = self._backend(self.decode_wrapper, "decode", self.d_indptr[: bs + 1], self.d_indices,
+                           self.d_last[:bs], self.d_batch[:bs], self.d_pos[:bs])
+        logits = self.model.forward(self.d_ids[:bs], self.d_pos[:bs], be)
+        return self.sampler.sample(logits, bs, out=self.sampler.out[:bs])
+
+    def _plan_decode(self, bs: int) -> None:
+        cfg = self.model.cfg
+        self.decode_wrapper.plan(self.d_indptr[: bs + 1], self.d_indices, self.d_last[:bs],
+                                 cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, self.page_size)
+
+    def _capture_graphs(self) -> None:
+        for bs in self.graph_sizes:
+            # all rows are padding rows: they own only the scratch page
+            self.pt.step([], [], bs, self.d_indptr, self.d_indices, self.d_last, self.d_batch, self.d_pos)
+            self._plan_decode(bs)
+            self.sampler.temperature[:bs].fill_(0.0)
+            s = torch.cuda.Stream(self.device)
+            s.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(s):
+                for _ in range(2):
+                    self._decode_forward(bs)
+            torch.cuda.current_stream(self.device).wait_stream(s)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                out = self._decode_forward(bs)
+            self.graphs[bs] = (g, out)
+        torch.cuda.synchronize(self.device)
+
+    # ------------------------------------------------------------------ step
+    def step(self) -> list[tuple[Request, int]]:
+        emitted: list[tuple[Request, int]] = []
+        admitted = self._admit()
+        if admitted:
+            emitted += self._prefill(admitted)
+        decoding = [r for r in self.active if r.status == RequestStatus.DECODING]
+        if decoding:
+            emitted += self._decode(decoding)
+        self._retire()
+        self.steps += 1
+        return emitted
+
+    def _admit(self) -> list[Request]:
+        out = []
+        while self.waiting and len(self.active) < self.max_batch_size:
+            req = self.waiting[0]
+            if len(req.input_ids) > self.max_seq_len:
+                raise ValueError(f"prompt of {len(req.input_ids)} tokens exceeds max_seq_len {self.max_seq_len}")
+            if not self.pt.can_admit(len(req.input_ids)):
+                break
+            self.waiting.popleft()
+            req.slot = self.free_slots.popleft()
+            req.status = RequestStatus.PREFILLING
+            self.active.append(req)
+            out.append(req)
+        return out
+
+    def _zero_released(self, n: int) -> None:
+        if n and self.zero_released:
+            self.kv.zero_pages(self.pt.released, n)
+
+    def _prefill(self, reqs: list[Request]) -> list[tuple[Request, int]]:
+        cfg = self.model.cfg
+        dev = self.device
+        admits = [(r.slot, self.pt.pages_needed(len(r.input_ids))) for r in reqs]
+        rows = [(r.slot, len(r.input_ids) - 1) for r in reqs]
+        n = len(reqs)
+        released = self.pt.step(admits, rows, n, self.p_indptr, self.p_indices, self.p_last,
+                                 self.p_batch_dummy, self.p_pos_dummy)
+        self._zero_released(released)
+        lens = [len(r.input_ids) for r in reqs]
+        qo = [0]
+        for x in lens:
+            qo.append(qo[-1] + x)
+        total = qo[-1]
+        ids = torch.tensor([t for r in reqs for t in r.input_ids], dtype=torch.int64).to(dev, non_blocking=True)
+        pos = torch.tensor([i for x in lens for i in range(x)], dtype=torch.int32).to(dev, non_blocking=True)
+        bidx = torch.tensor([b for b, x in enumerate(lens) for _ in range(x)], dtype=torch.int32).to(dev, non_blocking=True)
+        qo_d = torch.tensor(qo, dtype=torch.int32).to(dev, non_blocking=True)
+        last_rows = (qo_d[1:] - 1).to(torch.int64)
+        self.prefill_wrapper.plan(qo_d, self.p_indptr[: n + 1], self.p_indices, self.p_last[:n],
+                                  cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, self.page_size,
+                                  causal=True, max_total_q=total)
+        be = self._backend(self.prefill_wrapper, "prefill", self.p_indptr[: n + 1], self.p_indices,
+                           self.p_last[:n], bidx, pos)
+        logits = self.model.forward(ids, pos, be, last_rows=last_rows)
+        self.p_sampler.set_params([r.temperature for r in reqs], [r.top_p for r in reqs])
+        toks = self.p_sampler.sample(logits, n)
+        host = self._fetch(toks, n)
+        now = time.perf_counter()
+        out = []
+        for r, t in zip(reqs, host):
+            r.generated_tokens.append(t)
+            r.current_position = len(r.input_ids)
+            r.status = RequestStatus.DECODING
+            r.prefill_done_time = r.last_token_time = now
+            out.append((r, t))
+            if t in self.eos or len(r.generated_tokens) >= r.max_new_tokens:
+                r.status = RequestStatus.FINISHED
+                r.finish_reason = "stop" if t in self.eos else "length"
+        return out
+
+    def _decode(self, reqs: list[Request]) -> list[tuple[Request, int]]:
+        b = len(reqs)
+        bs = next((g for g in self.graph_sizes if g >= b), None)
+        graph = self.graphs.get(bs) if bs is not None else None
+        padded = bs if graph is not None else b
+        if padded > self.d_batch.numel():
+            raise RuntimeError(f"decode batch {b} exceeds the static buffers ({self.d_batch.numel()})")
+        rows = [(r.slot, r.current_position) for r in reqs]
+        released = self.pt.step([], rows, padded, self.d_indptr, self.d_indices, self.d_last, self.d_batch,
+                                self.d_pos)
+        self._zero_released(released)
+        self._up_ids.upload([r.generated_tokens[-1] for r in reqs] + [0] * (padded - b), self.d_ids)
+        self._up_t.upload([r.temperature for r in reqs] + [0.0] * (padded - b), self.sampler.temperature)
+        self._up_p.upload([r.top_p for r in reqs] + [1.0] * (padded - b), self.sampler.top_p)
+        self._plan_decode(padded)
+        if graph is not None:
+            g, out = graph
+            g.replay()
+            toks = out
+        else:
+            toks = self._decode_forward(padded)
+        host = self._fetch(toks, b)
+        now = time.perf_counter()
+        out_list = []
+        for r, t in zip(reqs, host):
+            r.generated_tokens.append(t)
+            r.current_position += 1
+            r.last_token_time = now
+            out_list.append((r, t))
+            if t in self.eos or len(r.generated_tokens) >= r.max_new_tokens or r.current_position >= self.max_seq_len:
+                r.status = RequestStatus.FINISHED
+                r.finish_reason = "stop" if t in self.eos else "length"
+        return out_list
+
+    def _fetch(self, toks: torch.Tensor, n: int) -> list[int]:
+        self._tok_host[:n].copy_(toks[:n], non_blocking=True)
+        torch.cuda.current_stream(self.device).synchronize()
+        return self._tok_host[:n].tolist()
+
+    def _retire(self) -> None:
+        still = []
+        for r in self.active:
+            if r.status == RequestStatus.FINISHED:
+                self.pt.release(r.slot)
+                self.free_slots.append(r.slot)
+            else:
+                still.append(r)
+        self.active = still

@@ -52,7 +52,7 @@ def test_host_only_calls_and_error_reporting():
                                 1, 2, 64, 16, None)
     assert rc == _lib.MI_ERR_INVALID
     assert "append" in _lib.last_error()
-    rc = lib.mi_decode_plan(None, 0, None, None, 1, 32, 8, 96, 16, 0, None)
+    rc = lib.mi_decode_plan(None, 0, None, None, None, 1, 32, 8, 96, 16, 0, None)
     assert rc == _lib.MI_ERR_UNSUPPORTED
-    rc = lib.mi_decode_plan(None, 0, None, None, 1, 32, 8, 128, 16, 0, None)
+    rc = lib.mi_decode_plan(None, 0, None, None, None, 1, 32, 8, 128, 16, 0, None)
     assert rc == _lib.MI_ERR_WORKSPACE

@@ -200,3 +200,16 @@ def test_rejects_unsupported(dev):
 
         small = BatchDecodeWithPagedKVCacheWrapper(torch.empty(1024, dtype=torch.uint8, device=dev))
         small.plan(ip, ix, lp, 32, 8, 128, 16)
+
+
+def test_golden_fixture_config1(dev):
+    """The kernel against the committed fp32 output of the config-1 case."""
+    from safetensors.torch import load_file
+
+    from tests.test_golden import FIX, load_pool
+
+    t = load_file(str(FIX))
+    w = _wrapper(dev)
+    w.plan(t["indptr"].to(dev), t["page_ids"].to(dev), t["last_page_len"].to(dev), 14, 2, 64, 16)
+    out = w.run(t["q"].to(dev), load_pool(t).to(dev)).float().cpu()
+    assert (out - t["out_fp32"]).abs().max().item() < TOL
