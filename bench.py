@@ -12,10 +12,13 @@ attention, sampler) and the read-back of the sampled ids.  ``value`` is
 decoded tokens per second over exactly ``--steps`` timed steps.
 
 ``roofline`` is measured on the decode-attention kernel alone: after the
-timed steps, the 32 layers' attention (the batch's real page tables and
-pools) is launched ``--attn-iters`` times on the current stream and bracketed
-with HIP events; achieved = algorithmic bytes per launch / average launch
-time.  ``cpu_baseline`` times the CPU oracle's gather-based attention on one
+timed steps, the 32 layers' attention launches (the batch's real page tables
+and pools, one pool per layer so nothing is served from the 256 MB Infinity
+Cache) are captured in a hipGraph, replayed ``--attn-iters`` times on the
+current stream and bracketed with HIP events; achieved = algorithmic bytes
+per launch / average launch time.  Algorithmic bytes per launch:
+sum_b kv_len_b * H_kv * D * 2 (K,V) * 2 B + 2 * B * H_q * D * 2 B (q, out)
++ 4 B * ((B+1) + sum_b npages_b + B) (indptr, indices, last_page_len).  ``cpu_baseline`` times the CPU oracle's gather-based attention on one
 layer of the same batch.
 """
 
@@ -51,6 +54,9 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--attn-iters", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 1 GiB device-to-device copy (5x): the known-traffic kernel used "
+                         "to scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the path runs on one MI355X); --gpus {args.gpus} "
@@ -58,6 +64,16 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.calibrate_copy:
+        n = (1 << 30) // 2
+        src = torch.ones(n, dtype=torch.bfloat16, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30, "launches": 5}))
+        return 0
 
     from __graft_entry__ import load_package
 
@@ -117,16 +133,26 @@ def main() -> int:
     outs = [torch.empty_like(q) for q in qs]
     npages = [math.ceil(n / 16) for n in kv_lens]
     alg_bytes = sum(kv_lens) * hkv * d * 2 * 2 + 2 * B * hq * d * 2 + 4 * ((B + 1) + sum(npages) + B)
-    for _ in range(2):
+    # The 32 launches are captured once and replayed, so the events time the
+    # kernels back to back on the GPU without host launch gaps.
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            for l in range(cfg.num_hidden_layers):
+                w.run(qs[l], sch.kv.kv_data[l], out=outs[l])
+    torch.cuda.current_stream().wait_stream(side)
+    attn_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(attn_graph):
         for l in range(cfg.num_hidden_layers):
             w.run(qs[l], sch.kv.kv_data[l], out=outs[l])
+    attn_graph.replay()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for _ in range(args.attn_iters):
-        for l in range(cfg.num_hidden_layers):
-            w.run(qs[l], sch.kv.kv_data[l], out=outs[l])
+        attn_graph.replay()
     e1.record(stream)
     e1.synchronize()
     launches = args.attn_iters * cfg.num_hidden_layers

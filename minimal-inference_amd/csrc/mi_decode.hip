@@ -161,29 +161,28 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
   __shared__ int red[16];
   __shared__ int scan[1024];
   const int t = threadIdx.x;
-  int tot = 0, mx = 0;
-  for (int b = t; b < p.batch; b += blockDim.x) {
-    const int np = max(0, p.indptr[b + 1] - p.indptr[b]);
-    tot += np;
-    mx = max(mx, np);
-  }
-  const int total_pages = block_sum(tot, red);
+  int mx = 0;
+  for (int b = t; b < p.batch; b += blockDim.x) mx = max(mx, p.indptr[b + 1] - p.indptr[b]);
   const int max_np = block_max(mx, red);
-  // Pages per item: aim at target_units units with at most kInlinePages
-  // pages per item; grow only if the workspace cannot hold that many items.
-  const long long want = (long long)total_pages * p.hkv;
-  int chunk = int((want + p.target_units - 1) / p.target_units);
-  chunk = min(max(chunk, 1), kInlinePages);
-  for (;;) {
+  // Pages per item ("chunk"): the smallest value whose items fit the limit,
+  // found by binary search (the item count is non-increasing in chunk).  The
+  // limit is one resident round of units (target_units / kv_heads items), so
+  // no wave runs a second unit -- or whole rounds when the batch alone needs
+  // more -- and never more items than the workspace holds.
+  const int round_items = max(1, p.target_units / p.hkv);
+  int limit = ((p.batch + round_items - 1) / round_items) * round_items;
+  limit = min(max(limit, 1), p.max_items);
+  int lo = 1, hi = max(max_np, 1);
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
     int cnt = 0;
     for (int b = t; b < p.batch; b += blockDim.x) {
       const int np = max(0, p.indptr[b + 1] - p.indptr[b]);
-      cnt += max(1, (np + chunk - 1) / chunk);
+      cnt += max(1, (np + mid - 1) / mid);
     }
-    const int items = block_sum(cnt, red);
-    if (items <= p.max_items || chunk >= max_np) break;
-    chunk *= 2;
+    if (block_sum(cnt, red) <= limit) hi = mid; else lo = mid + 1;
   }
+  const int chunk = lo;
   int running = 0;
   for (int base = 0; base < p.batch; base += blockDim.x) {
     const int b = base + t;
