@@ -228,16 +228,15 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
 // ------------------------------------------------------------------ run
 template <int D, int G>
 struct DecodeTraits {
-  static constexpr int KSTEPS = D / 32;  // MFMA k-steps for q.k
-  static constexpr int DL = 16;          // head_dim values per lane in P.V
-  static constexpr int LPT = D / DL;     // lanes per token row
-  static constexpr int TPP = 64 / LPT;   // tokens per pass
-  static constexpr int PASSES = kPageSize / TPP;
-  static constexpr int VL = DL / 8;   // 16-byte V loads per pass
-  static constexpr int OUT = D / 64;  // reduced outputs per head per lane
-  static constexpr int NBUF = (D <= 128) ? 3 : 2;  // pages held in registers
-  static_assert(TPP <= kPageSize && kPageSize % TPP == 0, "pass geometry");
-  static_assert(G >= 1 && G <= 8, "group size");
+  static constexpr int KSTEPS = D / 32;  // 16x16x32 MFMAs for S^T = K Q^T
+  static constexpr int NT = D / 16;      // 16-wide head_dim tiles for O += P V
+  static constexpr int CPR = D / 8;      // 16-byte chunks per token row of one head
+  static constexpr int LPI = CPR / 4;    // 16-byte loads per lane per page, for K and for V
+  static constexpr int RS = D * 2 + 16;  // LDS row stride in bytes (16 B pad spreads the banks)
+  static constexpr int SLOT = 2 * kPageSize * RS;  // one page of K and V in LDS
+  static constexpr int NBUF = (D <= 64) ? 3 : 2;  // pages held in registers
+  static constexpr int OUT = D / 64;                // merged outputs per head per lane
+  static_assert(G >= 1 && G <= 16, "group size");
 };
 
 struct RunParams {
@@ -259,8 +258,8 @@ struct RunParams {
 
 template <int D, int G>
 struct PageRegs {
-  uint4 k[DecodeTraits<D, G>::KSTEPS];
-  uint4 v[DecodeTraits<D, G>::PASSES][DecodeTraits<D, G>::VL];
+  uint4 k[DecodeTraits<D, G>::LPI];
+  uint4 v[DecodeTraits<D, G>::LPI];
 };
 
 template <typename F>
@@ -272,11 +271,42 @@ __device__ __forceinline__ void coherent_store(F* p, F v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
+typedef __attribute__((address_space(3))) char lds_t;
+
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
+__device__ __forceinline__ void lds_store16(lds_t* p, uint4 v) {
+  *(__attribute__((address_space(3))) u32x4_t*)p = __builtin_bit_cast(u32x4_t, v);
+}
+__device__ __forceinline__ uint4 lds_load16(const lds_t* p) {
+  return __builtin_bit_cast(uint4, *(const __attribute__((address_space(3))) u32x4_t*)p);
+}
+// gfx950 LDS transpose read: the 16 lanes of a group address 4 rows x 16
+// bf16 (lane j: row j/4, elements 4*(j%4)..+3) and lane j receives column j.
+__device__ __forceinline__ s16x4_t lds_read_tr16(const lds_t* p) {
+  typedef __attribute__((address_space(3))) bf16x4_t lds_v4;
+  return __builtin_bit_cast(s16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4*)p));
+}
+
+// One unit: (item, KV head).  Lane l of the wave is (g, j) = (l >> 4, l & 15).
+//
+//   page loads : 128 contiguous bytes per token row per instruction (8 lanes
+//                per row, 8 rows per instruction), staged in registers;
+//   LDS slot   : the page's K and V rows of this head, row-major with padding;
+//   S^T = K Q^T: 16x16x32 MFMAs; lane (g, j) reads K row j, d-chunk g + 4s
+//                from LDS (its A operand) and holds Q row j (head j) as B;
+//                it receives S^T[token 4g+i][head j];
+//   softmax    : per head j, lazy running max in the exp2 domain;
+//   O += P V   : 16x16x16 MFMAs; P[head j][token 4g+i] is exactly the S^T
+//                accumulator each lane already holds, and V comes from the
+//                LDS transpose read (lane (g, j) gets V[4g..4g+3][16t + j]);
+//                O[head 4g+i][16t + j] accumulates in registers.
 template <int D, int G>
-__device__ __forceinline__ void decode_unit(const RunParams& p, int u, float (*red)[D + 4]) {
+__device__ __forceinline__ void decode_unit(const RunParams& p, int u, lds_t* lds) {
   using T = DecodeTraits<D, G>;
   using Regs = PageRegs<D, G>;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
   const int item_idx = u / p.hkv;
   const int hkv = u - item_idx * p.hkv;
   const DecodeItem& itr = p.items[item_idx];
@@ -288,123 +318,100 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, float (*r
   const int64_t tok_stride = int64_t(p.hkv) * D;
   const int64_t kv_stride = kPageSize * tok_stride;
   const int64_t page_stride = 2 * kv_stride;
+  const int g = lane >> 4, j = lane & 15;
 
-  const int m = lane & 15, kb = lane >> 4;
-  const int tv = lane % T::TPP, cv = lane / T::TPP;
-  const int64_t k_off = int64_t(m) * tok_stride + int64_t(hkv) * D + kb * 8;
-  const int64_t v_off = kv_stride + int64_t(tv) * tok_stride + int64_t(hkv) * D + cv * 8;
-
-  // Loads are unconditional so the compiler can keep them in flight across
-  // the page loop: an invalid page id reads page 0 and is masked in consume.
+  // load lane geometry: instruction i covers rows (lane & 7) + 8 * (i & 1),
+  // chunk (lane >> 3) + 8 * (i >> 1)
+  const int lrow = lane & 7, lchunk = lane >> 3;
+  const int64_t ld_off = int64_t(lrow) * tok_stride + int64_t(hkv) * D + lchunk * 8;
   auto load_page = [&](Regs& r, int page) {
     const int safe = (page >= 0 && page < p.num_pages) ? page : 0;
-    const uint16_t* pg = p.pool + int64_t(safe) * page_stride;
+    const uint16_t* pg = p.pool + int64_t(safe) * page_stride + ld_off;
 #pragma unroll
-    for (int s = 0; s < T::KSTEPS; ++s) r.k[s] = mi::load16(pg + k_off + s * 32);
-#pragma unroll
-    for (int ps = 0; ps < T::PASSES; ++ps)
-#pragma unroll
-      for (int j = 0; j < T::VL; ++j)
-        r.v[ps][j] = mi::load16(pg + v_off + int64_t(ps * T::TPP) * tok_stride + j * (T::LPT * 8));
+    for (int i = 0; i < T::LPI; ++i) {
+      const int64_t o = int64_t(8 * (i & 1)) * tok_stride + 64 * (i >> 1);
+      r.k[i] = mi::load16(pg + o);
+      r.v[i] = mi::load16(pg + kv_stride + o);
+    }
   };
 
-  // Q as the A operand: row m = head within the group.
-  mi::bf16x8_t qa[T::KSTEPS];
+  // Q^T as the B operand: column j = head j of the group (zero when j >= G)
+  mi::bf16x8_t qb[T::KSTEPS];
   {
-    const uint16_t* qrow = p.q + int64_t(b) * p.q_sb + int64_t(hkv * G + (m < G ? m : 0)) * p.q_sh + kb * 8;
+    const uint16_t* qrow = p.q + int64_t(b) * p.q_sb + int64_t(hkv * G + (j < G ? j : 0)) * p.q_sh + g * 8;
 #pragma unroll
     for (int s = 0; s < T::KSTEPS; ++s) {
       uint4 v = mi::load16(qrow + s * 32);
-      if (m >= G) v = make_uint4(0, 0, 0, 0);
-      qa[s] = mi::as_bf16x8(v);
+      if (j >= G) v = make_uint4(0, 0, 0, 0);
+      qb[s] = mi::as_bf16x8(v);
     }
   }
 
-  float acc[G][T::DL];
+  mi::f32x4_t acc[T::NT];
 #pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int j = 0; j < T::DL; ++j) acc[h][j] = 0.f;
-  float mh[G];
-#pragma unroll
-  for (int h = 0; h < G; ++h) mh[h] = -INFINITY;
-  float lrow[4] = {0.f, 0.f, 0.f, 0.f};
-  const int row = lane >> 4;  // S-layout row group: heads 4*row .. 4*row+3
+  for (int t = 0; t < T::NT; ++t) acc[t] = mi::f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;  // head j
+  float l_run = 0.f;        // head j, this lane's tokens
 
-  // valid: tokens of the page that take part (0 for an invalid page id)
+  lds_t* kl = lds;
+  lds_t* vl = lds + kPageSize * T::RS;
+
   auto consume = [&](const Regs& r, int valid) {
-    // ---- S = Q K^T (lane: heads 4*row+i, token lane&15)
+    // ---- stage the page in LDS (V rows past `valid` as zeros: P is 0 there,
+    // but 0 * NaN would poison the MFMA)
+#pragma unroll
+    for (int i = 0; i < T::LPI; ++i) {
+      const int row = lrow + 8 * (i & 1);
+      const int chunk = lchunk + 8 * (i >> 1);
+      lds_store16(kl + row * T::RS + chunk * 16, r.k[i]);
+      lds_store16(vl + row * T::RS + chunk * 16, (row < valid) ? r.v[i] : make_uint4(0, 0, 0, 0));
+    }
+    // ---- S^T = K Q^T
     mi::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < T::KSTEPS; ++s) c = mi::mfma_16x16x32_bf16(qa[s], mi::as_bf16x8(r.k[s]), c);
-    const int tok = lane & 15;
-    float s2[4];
+    for (int s = 0; s < T::KSTEPS; ++s) {
+      const uint4 ka = lds_load16(kl + j * T::RS + (g + 4 * s) * 16);
+      c = mi::mfma_16x16x32_bf16(mi::as_bf16x8(ka), qb[s], c);
+    }
+    float sv[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s2[i] = (tok < valid) ? c[i] * p.scale_log2 : -INFINITY;
-
-    // ---- page max per head, lazy rescale
-    float rm[4];
+    for (int i = 0; i < 4; ++i) sv[i] = (4 * g + i < valid) ? c[i] * p.scale_log2 : -INFINITY;
+    // ---- online softmax for head j, lazy rescale
+    float mloc = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    mloc = fmaxf(mloc, mi::lane_shuffle(mloc, lane ^ 16));
+    mloc = fmaxf(mloc, mi::lane_shuffle(mloc, lane ^ 32));
+    const bool need = mloc > m_run + kLazyRescale;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+      const float mnew = need ? mloc : m_run;
+      const float f = need ? ((m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - mnew)) : 1.f;
+      m_run = mnew;
+      l_run *= f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) rm[i] = mi::group16_max(s2[i]);
-    float mp[G];
+      for (int i = 0; i < 4; ++i) {
+        const float fo = mi::lane_shuffle(f, 4 * g + i);
 #pragma unroll
-    for (int h = 0; h < G; ++h) mp[h] = mi::read_lane(rm[h & 3], (h >> 2) * 16);
-    bool need = false;
-#pragma unroll
-    for (int h = 0; h < G; ++h) need |= (mp[h] > mh[h] + kLazyRescale);
-    if (need) {
-      float f[8];
-#pragma unroll
-      for (int h = 0; h < 8; ++h) f[h] = 1.f;
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        if (mp[h] > mh[h] + kLazyRescale) {
-          f[h] = (mh[h] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mh[h] - mp[h]);
-          mh[h] = mp[h];
-#pragma unroll
-          for (int j = 0; j < T::DL; ++j) acc[h][j] *= f[h];
-        }
+        for (int t = 0; t < T::NT; ++t) acc[t][i] *= fo;
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) lrow[i] *= (row == 0) ? f[i] : f[4 + i];
     }
-    float pS[4];
+    float pv[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float mm = 0.f;
-      if (i < G) mm = mh[i];
-      if (row == 1 && 4 + i < G) mm = mh[(4 + i < G) ? 4 + i : 0];
-      pS[i] = (s2[i] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(s2[i] - mm);
-      lrow[i] += pS[i];
-    }
-
+    for (int i = 0; i < 4; ++i) pv[i] = (sv[i] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(sv[i] - m_run);
+    l_run += (pv[0] + pv[1]) + (pv[2] + pv[3]);
+    const uint32_t p01 = mi::pack_bf16x2(pv[0], pv[1]), p23 = mi::pack_bf16x2(pv[2], pv[3]);
+    s16x4_t pa;
+    pa[0] = short(p01 & 0xffff);
+    pa[1] = short(p01 >> 16);
+    pa[2] = short(p23 & 0xffff);
+    pa[3] = short(p23 >> 16);
     // ---- O += P V
+    const lds_t* vrow = vl + (4 * g + (j >> 2)) * T::RS + (j & 3) * 8;
 #pragma unroll
-    for (int ps = 0; ps < T::PASSES; ++ps) {
-      const int tsrc = tv + ps * T::TPP;
-      float pv[G];
-#pragma unroll
-      for (int h = 0; h < G; ++h) pv[h] = mi::lane_shuffle(pS[h & 3], (h >> 2) * 16 + tsrc);
-      const bool vmask = tsrc >= valid;
-#pragma unroll
-      for (int j = 0; j < T::VL; ++j) {
-        uint4 v = r.v[ps][j];
-        if (vmask) v = make_uint4(0, 0, 0, 0);
-        const float vf[8] = {mi::bf16_lo(v.x), mi::bf16_hi(v.x), mi::bf16_lo(v.y), mi::bf16_hi(v.y),
-                             mi::bf16_lo(v.z), mi::bf16_hi(v.z), mi::bf16_lo(v.w), mi::bf16_hi(v.w)};
-#pragma unroll
-        for (int h = 0; h < G; ++h)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[h][j * 8 + e] = fmaf(pv[h], vf[e], acc[h][j * 8 + e]);
-      }
-    }
+    for (int t = 0; t < T::NT; ++t)
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, lds_read_tr16(vrow + 32 * t), acc[t], 0, 0, 0);
   };
 
-  // ---- stream the pages in groups of kInlinePages.  Lane j of `pid` holds
-  // the group's j-th page id (the item's inline copy for group 0), read once
-  // per group; v_readlane then yields wave-uniform ids without further memory
-  // waits.  Inside a group the loop is unrolled so NBUF-1 pages are in
-  // flight while one is consumed.
+  // ---- stream the pages in groups of kInlinePages (ids: item inline copy
+  // for group 0, kv_indices after), NBUF-1 pages in flight in registers
   for (int g0 = 0; g0 < npg; g0 += kInlinePages) {
     const int cnt = min(kInlinePages, npg - g0);
     int pid = -1;
@@ -423,46 +430,27 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, float (*r
     }
   }
 
-  // ---- softmax denominators (wave-uniform per head)
-  float lh[G];
-  {
-    float ls[4];
+  // ---- per-head denominators; O rows are heads 4g + i
+  float lt = l_run + mi::lane_shuffle(l_run, lane ^ 16);
+  lt += mi::lane_shuffle(lt, lane ^ 32);
+  float lo[4], mo[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ls[i] = mi::group16_sum(lrow[i]);
-#pragma unroll
-    for (int h = 0; h < G; ++h) lh[h] = mi::read_lane(ls[h & 3], (h >> 2) * 16);
+  for (int i = 0; i < 4; ++i) {
+    lo[i] = mi::lane_shuffle(lt, 4 * g + i);
+    mo[i] = mi::lane_shuffle(m_run, 4 * g + i);
   }
-
-  // ---- reduce acc over the TPP token lanes through LDS
-  float o[G][T::OUT];
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-#pragma unroll
-    for (int j = 0; j < T::VL; ++j) {
-      float* dst = &red[tv][j * (T::LPT * 8) + cv * 8];
-      *reinterpret_cast<float4*>(dst) =
-          make_float4(acc[h][j * 8 + 0], acc[h][j * 8 + 1], acc[h][j * 8 + 2], acc[h][j * 8 + 3]);
-      *reinterpret_cast<float4*>(dst + 4) =
-          make_float4(acc[h][j * 8 + 4], acc[h][j * 8 + 5], acc[h][j * 8 + 6], acc[h][j * 8 + 7]);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < T::OUT; ++k) {
-      float sum = 0.f;
-#pragma unroll
-      for (int t = 0; t < T::TPP; ++t) sum += red[t][lane + 64 * k];
-      o[h][k] = sum;
-    }
-    __syncthreads();
-  }
+  (void)mo;
 
   if (nsplit == 1) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float inv = lh[h] > 0.f ? 1.f / lh[h] : 0.f;
-      uint16_t* orow = p.out + int64_t(b) * p.o_sb + int64_t(hkv * G + h) * p.o_sh;
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * g + i;
+      if (h < G) {
+        const float inv = lo[i] > 0.f ? 1.f / lo[i] : 0.f;
+        uint16_t* orow = p.out + int64_t(b) * p.o_sb + int64_t(hkv * G + h) * p.o_sh + j;
 #pragma unroll
-      for (int k = 0; k < T::OUT; ++k) orow[lane + 64 * k] = mi::f32_to_bf16(o[h][k] * inv);
+        for (int t = 0; t < T::NT; ++t) orow[16 * t] = mi::f32_to_bf16(acc[t][i] * inv);
+      }
     }
     return;
   }
@@ -471,19 +459,16 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, float (*r
   {
     float* po = p.po + int64_t(u) * G * D;
 #pragma unroll
-    for (int h = 0; h < G; ++h)
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * g + i;
+      if (h < G) {
 #pragma unroll
-      for (int k = 0; k < T::OUT; ++k) coherent_store(po + h * D + lane + 64 * k, o[h][k]);
-    if (lane < G) {
-      float mv = 0.f, lv = 0.f;
-#pragma unroll
-      for (int h = 0; h < G; ++h)
-        if (lane == h) {
-          mv = mh[h];
-          lv = lh[h];
-        }
-      coherent_store(p.pml + (int64_t(u) * G + lane) * 2 + 0, mv);
-      coherent_store(p.pml + (int64_t(u) * G + lane) * 2 + 1, lv);
+        for (int t = 0; t < T::NT; ++t) coherent_store(po + h * D + 16 * t + j, acc[t][i]);
+      }
+    }
+    if (lane < G) {  // lane h holds m_run / lt of head h
+      coherent_store(p.pml + (int64_t(u) * G + lane) * 2 + 0, m_run);
+      coherent_store(p.pml + (int64_t(u) * G + lane) * 2 + 1, lt);
     }
   }
   // Wait until this wave's write-through stores are acknowledged (vmcnt 0;
@@ -565,11 +550,16 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, float (*r
   if (lane == 0) coherent_store(counter, 0);
 }
 
+// head_dim <= 128: registers capped at 256 per wave (double-buffered pages
+// need ~160-200), so at least two waves share a SIMD; measured faster than a
+// deeper per-wave prefetch at lower occupancy.  head_dim 256 needs the full
+// register file for two pages in flight.
 template <int D, int G>
-__global__ __launch_bounds__(64) void decode_run_kernel(RunParams p) {
-  __shared__ float red[DecodeTraits<D, G>::TPP][D + 4];
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void decode_run_kernel(RunParams p) {
+  __shared__ __attribute__((aligned(16))) char slot[DecodeTraits<D, G>::SLOT];
+  lds_t* lds = (lds_t*)slot;
   const int num_units = p.header->num_units;
-  for (int u = blockIdx.x; u < num_units; u += gridDim.x) decode_unit<D, G>(p, u, red);
+  for (int u = blockIdx.x; u < num_units; u += gridDim.x) decode_unit<D, G>(p, u, lds);
 }
 
 typedef void (*RunKernel)(RunParams);
