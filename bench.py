@@ -18,8 +18,16 @@ Cache) are captured in a hipGraph, replayed ``--attn-iters`` times on the
 current stream and bracketed with HIP events; achieved = algorithmic bytes
 per launch / average launch time.  Algorithmic bytes per launch:
 sum_b kv_len_b * H_kv * D * 2 (K,V) * 2 B + 2 * B * H_q * D * 2 B (q, out)
-+ 4 B * ((B+1) + sum_b npages_b + B) (indptr, indices, last_page_len).  ``cpu_baseline`` times the CPU oracle's gather-based attention on one
-layer of the same batch.
++ 4 B * ((B+1) + sum_b npages_b + B) (indptr, indices, last_page_len).
+
+``roofline.traffic`` is the HBM bytes per launch that rocprofv3 counted for
+this same attention leg (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled
+by what the counter reads for a 1 GiB device copy), read from
+profiles/decode_attn_traffic.json when that file was measured on this
+workload (same model, batch and mean context); otherwise null.
+
+``cpu_baseline`` times the CPU oracle's gather-based attention on one layer of
+the same batch.
 """
 
 from __future__ import annotations
@@ -37,11 +45,26 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBPS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "decode_attn_traffic.json"
 PUBLISHED_TOKS = 1532.0  # reference README.md:56, H100, 32 concurrent, aggregate tok/s
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def measured_traffic(model: str, batch: int, mean_context: float):
+    """HBM bytes per attention launch from the committed counter summary, or
+    None when it was measured on another workload."""
+    try:
+        rec = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    if rec.get("model") != model or rec.get("batch") != batch:
+        return None
+    if abs(float(rec.get("mean_context", -1)) - mean_context) > 0.05:
+        return None
+    return float(rec["traffic_bytes"])
 
 
 def main() -> int:
@@ -193,6 +216,8 @@ def main() -> int:
                          f"{med * 1000:.1f} ms per layer"}
         log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
 
+    mean_ctx = round(sum(kv_lens) / B, 1)
+    traffic = measured_traffic(args.model, B, mean_ctx)
     line = {
         "metric": "decode-attn HBM GB/s (% of peak) + decode tok/s, Mistral-7B B=32",
         "value": round(toks, 2),
@@ -208,11 +233,11 @@ def main() -> int:
         "data": "synthetic (random-init weights, random prompt token ids)",
         "config": {"workload": f"{args.model} decode, B={B}, prompts U[128,1024] seed {args.seed}, "
                                f"half greedy / half T=0.7 top-p 0.9, page_size 16, hipGraph decode",
-                   "batch": B, "mean_context": round(sum(kv_lens) / B, 1), "parallelism": "single GPU"},
+                   "batch": B, "mean_context": mean_ctx, "parallelism": "single GPU"},
         "decode_attn_us": round(attn_us, 3),
         "decode_attn_gbps": round(achieved, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": None},
+                     "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -43,21 +43,40 @@ constexpr float kLazyRescale = 8.0f;  // log2 units
 #define MI_DECODE_UNITS_PER_CU 8
 #endif
 constexpr int kUnitsPerCU = MI_DECODE_UNITS_PER_CU;
-constexpr int kInlinePages = 8;
+#ifndef MI_DECODE_NB128
+#define MI_DECODE_NB128 4
+#endif
+#ifndef MI_DECODE_NB64
+#define MI_DECODE_NB64 8
+#endif
+#ifndef MI_DECODE_WAVES
+#define MI_DECODE_WAVES 2
+#endif
+#ifndef MI_DECODE_KB_REGS
+#define MI_DECODE_KB_REGS 96
+#endif
+constexpr int kInlinePages = 24;
 // s_waitcnt immediate (gfx9 encoding): vmcnt = 0, expcnt = 7, lgkmcnt = 15.
 constexpr int kWaitVmcnt0 = 0x0F70;
+// Buffer resource word 3 for gfx9 raw buffers (32-bit data format, no swizzle).
+constexpr int kBufferWord3 = 0x00020000;
 
-struct alignas(64) DecodeItem {
-  int b;           // request
-  int page_begin;  // absolute position in kv_indices
+// One item = a contiguous page range of one request.  Read by a wave with one
+// 4-byte load per lane (lane l gets word l), so the page ids come first.
+struct alignas(128) DecodeItem {
+  int pages[kInlinePages];  // kv_indices[page_begin ..] copied by plan(), -1 past the end
+  int b;                    // request
+  int page_begin;           // absolute position in kv_indices
   int page_end;
   int last_valid;  // valid tokens in the item's final page (0 when empty)
   int split;
   int nsplit;
   int item_base;  // item index of split 0 of this request
   int pad;
-  int pages[kInlinePages];  // kv_indices[page_begin ..] copied by plan()
 };
+static_assert(sizeof(DecodeItem) == 128, "item is read as 32 lanes x 4 bytes");
+constexpr int kItemB = kInlinePages, kItemBegin = kInlinePages + 1, kItemEnd = kInlinePages + 2,
+              kItemLast = kInlinePages + 3, kItemNsplit = kInlinePages + 5, kItemBase = kInlinePages + 6;
 
 struct DecodeHeader {
   int num_units;
@@ -234,9 +253,14 @@ struct DecodeTraits {
   static constexpr int LPI = CPR / 4;    // 16-byte loads per lane per page, for K and for V
   static constexpr int RS = D * 2 + 16;  // LDS row stride in bytes (16 B pad spreads the banks)
   static constexpr int SLOT = 2 * kPageSize * RS;  // one page of K and V in LDS
-  static constexpr int NBUF = (D <= 64) ? 3 : 2;  // pages held in registers
-  static constexpr int OUT = D / 64;                // merged outputs per head per lane
+  // Pages in flight per wave (~128-160 registers of staging).
+  static constexpr int NB = (D == 64) ? MI_DECODE_NB64 : (D == 128) ? MI_DECODE_NB128 : 2;
+  static constexpr int OUT = D / 64;  // merged outputs per head per lane
+  // Splits whose partial rows one merge batch loads together (<= 96 registers).
+  static constexpr int KB_RAW = MI_DECODE_KB_REGS / (G * OUT);
+  static constexpr int KB = KB_RAW > 16 ? 16 : (KB_RAW < 1 ? 1 : KB_RAW);
   static_assert(G >= 1 && G <= 16, "group size");
+  static_assert((NB - 1) * 2 * LPI <= 63, "vmcnt range");
 };
 
 struct RunParams {
@@ -247,19 +271,22 @@ struct RunParams {
   float* po;
   const uint16_t* q;
   int64_t q_sb, q_sh;
-  const uint16_t* pool;
+  const char* pool;
   int64_t num_pages;
   const int32_t* indices;
   uint16_t* out;
   int64_t o_sb, o_sh;
   int hkv;
+  int max_items;
   float scale_log2;
 };
 
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
+
 template <int D, int G>
 struct PageRegs {
-  uint4 k[DecodeTraits<D, G>::LPI];
-  uint4 v[DecodeTraits<D, G>::LPI];
+  u32x4_t k[DecodeTraits<D, G>::LPI];
+  u32x4_t v[DecodeTraits<D, G>::LPI];
 };
 
 template <typename F>
@@ -275,12 +302,11 @@ typedef __attribute__((ext_vector_type(4))) short s16x4_t;
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
 typedef __attribute__((address_space(3))) char lds_t;
 
-typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
-__device__ __forceinline__ void lds_store16(lds_t* p, uint4 v) {
-  *(__attribute__((address_space(3))) u32x4_t*)p = __builtin_bit_cast(u32x4_t, v);
+__device__ __forceinline__ void lds_store16(lds_t* p, u32x4_t v) {
+  *(__attribute__((address_space(3))) u32x4_t*)p = v;
 }
-__device__ __forceinline__ uint4 lds_load16(const lds_t* p) {
-  return __builtin_bit_cast(uint4, *(const __attribute__((address_space(3))) u32x4_t*)p);
+__device__ __forceinline__ u32x4_t lds_load16(const lds_t* p) {
+  return *(const __attribute__((address_space(3))) u32x4_t*)p;
 }
 // gfx950 LDS transpose read: the 16 lanes of a group address 4 rows x 16
 // bf16 (lane j: row j/4, elements 4*(j%4)..+3) and lane j receives column j.
@@ -289,10 +315,47 @@ __device__ __forceinline__ s16x4_t lds_read_tr16(const lds_t* p) {
   return __builtin_bit_cast(s16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4*)p));
 }
 
+typedef __attribute__((ext_vector_type(4))) float f32x4_v;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4_v;
+
+// Max / sum of x and its value in lane ^ 16 (resp. lane ^ 32), with the
+// gfx950 lane-swap instructions: swapping x with itself leaves x in one
+// result and the partner's x in the other, for every lane.
+__device__ __forceinline__ float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// Wave-wide max / sum, every lane gets the result (no LDS traffic).
+__device__ __forceinline__ float wave_max_fast(float x) { return max_xor32(max_xor16(mi::group16_max(x))); }
+__device__ __forceinline__ float wave_sum_fast(float x) { return sum_xor32(sum_xor16(mi::group16_sum(x))); }
+
+// Word (lane & 31) of the item of unit u.  The index is clamped to the item
+// array, so the read is in bounds even before the unit count is known.
+__device__ __forceinline__ int load_item_word(const RunParams& p, int u) {
+  const int idx = min(u / p.hkv, p.max_items - 1);
+  return reinterpret_cast<const int*>(p.items + idx)[threadIdx.x & 31];
+}
+
 // One unit: (item, KV head).  Lane l of the wave is (g, j) = (l >> 4, l & 15).
 //
-//   page loads : 128 contiguous bytes per token row per instruction (8 lanes
-//                per row, 8 rows per instruction), staged in registers;
+//   page loads : raw buffer loads through a per-page descriptor (base = the
+//                page, size = the page, or size 0 for a missing / invalid
+//                page, whose loads then return zeros without touching
+//                memory); 128 contiguous bytes per token row per instruction
+//                (8 lanes per row, 8 rows per instruction); NB pages in
+//                flight in registers, issued NB pages ahead of use;
 //   LDS slot   : the page's K and V rows of this head, row-major with padding;
 //   S^T = K Q^T: 16x16x32 MFMAs; lane (g, j) reads K row j, d-chunk g + 4s
 //                from LDS (its A operand) and holds Q row j (head j) as B;
@@ -303,49 +366,61 @@ __device__ __forceinline__ s16x4_t lds_read_tr16(const lds_t* p) {
 //                LDS transpose read (lane (g, j) gets V[4g..4g+3][16t + j]);
 //                O[head 4g+i][16t + j] accumulates in registers.
 template <int D, int G>
-__device__ __forceinline__ void decode_unit(const RunParams& p, int u, lds_t* lds) {
+__device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, lds_t* lds) {
   using T = DecodeTraits<D, G>;
   using Regs = PageRegs<D, G>;
   const int lane = threadIdx.x & 63;
-  const int item_idx = u / p.hkv;
-  const int hkv = u - item_idx * p.hkv;
-  const DecodeItem& itr = p.items[item_idx];
-  const int b = itr.b;
-  const int page_begin = itr.page_begin, page_end = itr.page_end, last_valid = itr.last_valid;
-  const int nsplit = itr.nsplit, item_base = itr.item_base;
-  const int npg = page_end - page_begin;
-
-  const int64_t tok_stride = int64_t(p.hkv) * D;
-  const int64_t kv_stride = kPageSize * tok_stride;
-  const int64_t page_stride = 2 * kv_stride;
+  const int hkv = u - (u / p.hkv) * p.hkv;
+  const int b = mi::read_lane_i(iv, kItemB);
+  const int page_begin = mi::read_lane_i(iv, kItemBegin);
+  const int npg = mi::read_lane_i(iv, kItemEnd) - page_begin;
+  const int last_valid = mi::read_lane_i(iv, kItemLast);
+  const int nsplit = mi::read_lane_i(iv, kItemNsplit);
+  const int item_base = mi::read_lane_i(iv, kItemBase);
   const int g = lane >> 4, j = lane & 15;
 
-  // load lane geometry: instruction i covers rows (lane & 7) + 8 * (i & 1),
-  // chunk (lane >> 3) + 8 * (i >> 1)
-  const int lrow = lane & 7, lchunk = lane >> 3;
-  const int64_t ld_off = int64_t(lrow) * tok_stride + int64_t(hkv) * D + lchunk * 8;
-  auto load_page = [&](Regs& r, int page) {
-    const int safe = (page >= 0 && page < p.num_pages) ? page : 0;
-    const uint16_t* pg = p.pool + int64_t(safe) * page_stride + ld_off;
-#pragma unroll
-    for (int i = 0; i < T::LPI; ++i) {
-      const int64_t o = int64_t(8 * (i & 1)) * tok_stride + 64 * (i >> 1);
-      r.k[i] = mi::load16(pg + o);
-      r.v[i] = mi::load16(pg + kv_stride + o);
-    }
-  };
-
-  // Q^T as the B operand: column j = head j of the group (zero when j >= G)
+  // Q^T as the B operand: column j = head j of the group (zero when j >= G:
+  // those lanes read out of the descriptor's range, which returns zeros, so
+  // the loads are unconditional and nothing waits on them early).
   mi::bf16x8_t qb[T::KSTEPS];
   {
-    const uint16_t* qrow = p.q + int64_t(b) * p.q_sb + int64_t(hkv * G + (j < G ? j : 0)) * p.q_sh + g * 8;
+    const uint16_t* q0 = p.q + int64_t(b) * p.q_sb + int64_t(hkv * G) * p.q_sh;
+    const int q_bytes = int((G - 1) * p.q_sh * 2) + D * 2;
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)q0, (short)0, q_bytes, kBufferWord3);
+    const int qoff = (j < G) ? int(j * p.q_sh * 2) + g * 16 : 0x7ffffff0;
 #pragma unroll
-    for (int s = 0; s < T::KSTEPS; ++s) {
-      uint4 v = mi::load16(qrow + s * 32);
-      if (j >= G) v = make_uint4(0, 0, 0, 0);
-      qb[s] = mi::as_bf16x8(v);
-    }
+    for (int s = 0; s < T::KSTEPS; ++s)
+      qb[s] = __builtin_bit_cast(mi::bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(rq, qoff, s * 64, 0));
   }
+
+  // Byte offsets inside a page: lane part (voffset) and instruction part
+  // (soffset).  Load i covers token rows (lane & 7) + 8 * (i & 1) and 16-byte
+  // chunk (lane >> 3) + 8 * (i >> 1): 128 contiguous bytes per row, which
+  // streams measurably faster than the 64 bytes per row an MFMA operand
+  // layout would allow.
+  const int tok_bytes = p.hkv * D * 2;
+  const int kv_bytes = kPageSize * tok_bytes;
+  const int page_bytes = 2 * kv_bytes;
+  const int lrow = lane & 7, lchunk = lane >> 3;
+  const int voff = lrow * tok_bytes + hkv * D * 2 + lchunk * 16;
+
+  int pidv = iv;  // page ids of the current group, lane k = page k of the group
+
+  auto page_id = [&](int k) { return __builtin_amdgcn_readlane(pidv, k & 63); };
+  auto page_ok = [&](int k, int pg, int gsize) { return k < gsize && pg >= 0 && pg < p.num_pages; };
+  auto issue = [&](Regs& r, int k, int gsize) {
+    const int pg = page_id(k);
+    const bool ok = page_ok(k, pg, gsize);
+    const char* base = ok ? p.pool + int64_t(pg) * page_bytes : p.pool;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, ok ? page_bytes : 0, kBufferWord3);
+#pragma unroll
+    for (int i = 0; i < T::LPI; ++i) {
+      const int so = 8 * (i & 1) * tok_bytes + 128 * (i >> 1);
+      r.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, so, 0);
+      r.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, so + kv_bytes, 0);
+    }
+  };
 
   mi::f32x4_t acc[T::NT];
 #pragma unroll
@@ -357,29 +432,35 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, lds_t* ld
   lds_t* vl = lds + kPageSize * T::RS;
 
   auto consume = [&](const Regs& r, int valid) {
-    // ---- stage the page in LDS (V rows past `valid` as zeros: P is 0 there,
-    // but 0 * NaN would poison the MFMA)
+    // ---- the page to LDS (V rows past `valid` as zeros on a partial page:
+    // P is 0 there, but 0 * NaN would poison the MFMA)
 #pragma unroll
-    for (int i = 0; i < T::LPI; ++i) {
-      const int row = lrow + 8 * (i & 1);
-      const int chunk = lchunk + 8 * (i >> 1);
-      lds_store16(kl + row * T::RS + chunk * 16, r.k[i]);
-      lds_store16(vl + row * T::RS + chunk * 16, (row < valid) ? r.v[i] : make_uint4(0, 0, 0, 0));
+    for (int i = 0; i < T::LPI; ++i)
+      lds_store16(kl + (lrow + 8 * (i & 1)) * T::RS + (lchunk + 8 * (i >> 1)) * 16, r.k[i]);
+    if (valid == kPageSize) {
+#pragma unroll
+      for (int i = 0; i < T::LPI; ++i)
+        lds_store16(vl + (lrow + 8 * (i & 1)) * T::RS + (lchunk + 8 * (i >> 1)) * 16, r.v[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < T::LPI; ++i) {
+        const int row = lrow + 8 * (i & 1);
+        lds_store16(vl + row * T::RS + (lchunk + 8 * (i >> 1)) * 16, (row < valid) ? r.v[i] : u32x4_t{0, 0, 0, 0});
+      }
     }
     // ---- S^T = K Q^T
     mi::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < T::KSTEPS; ++s) {
-      const uint4 ka = lds_load16(kl + j * T::RS + (g + 4 * s) * 16);
-      c = mi::mfma_16x16x32_bf16(mi::as_bf16x8(ka), qb[s], c);
-    }
+    for (int s = 0; s < T::KSTEPS; ++s)
+      c = mi::mfma_16x16x32_bf16(__builtin_bit_cast(mi::bf16x8_t, lds_load16(kl + j * T::RS + (g + 4 * s) * 16)),
+                                 qb[s], c);
     float sv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) sv[i] = (4 * g + i < valid) ? c[i] * p.scale_log2 : -INFINITY;
     // ---- online softmax for head j, lazy rescale
     float mloc = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    mloc = fmaxf(mloc, mi::lane_shuffle(mloc, lane ^ 16));
-    mloc = fmaxf(mloc, mi::lane_shuffle(mloc, lane ^ 32));
+    mloc = max_xor16(mloc);
+    mloc = max_xor32(mloc);
     const bool need = mloc > m_run + kLazyRescale;
     if (__builtin_amdgcn_ballot_w64(need)) {
       const float mnew = need ? mloc : m_run;
@@ -393,16 +474,15 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, lds_t* ld
         for (int t = 0; t < T::NT; ++t) acc[t][i] *= fo;
       }
     }
+    // exp2(-inf - m) = 0 for masked tokens; m is taken as 0 while no token
+    // of the head has been seen (m_run still -inf), avoiding -inf - -inf
+    const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
     float pv[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pv[i] = (sv[i] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(sv[i] - m_run);
+    for (int i = 0; i < 4; ++i) pv[i] = __builtin_amdgcn_exp2f(sv[i] - m_use);
     l_run += (pv[0] + pv[1]) + (pv[2] + pv[3]);
-    const uint32_t p01 = mi::pack_bf16x2(pv[0], pv[1]), p23 = mi::pack_bf16x2(pv[2], pv[3]);
-    s16x4_t pa;
-    pa[0] = short(p01 & 0xffff);
-    pa[1] = short(p01 >> 16);
-    pa[2] = short(p23 & 0xffff);
-    pa[3] = short(p23 >> 16);
+    const s16x4_t pa = __builtin_bit_cast(
+        s16x4_t, __builtin_convertvector((f32x4_v){pv[0], pv[1], pv[2], pv[3]}, bf16x4_v));
     // ---- O += P V
     const lds_t* vrow = vl + (4 * g + (j >> 2)) * T::RS + (j & 3) * 8;
 #pragma unroll
@@ -410,36 +490,49 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, lds_t* ld
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, lds_read_tr16(vrow + 32 * t), acc[t], 0, 0, 0);
   };
 
-  // ---- stream the pages in groups of kInlinePages (ids: item inline copy
-  // for group 0, kv_indices after), NBUF-1 pages in flight in registers
-  for (int g0 = 0; g0 < npg; g0 += kInlinePages) {
-    const int cnt = min(kInlinePages, npg - g0);
-    int pid = -1;
-    if (lane < cnt) pid = (g0 == 0) ? itr.pages[lane] : p.indices[page_begin + g0 + lane];
-    Regs buf[T::NBUF];
+  // ---- stream the pages: groups of page ids (the item's inline copy first,
+  // then 64 at a time from kv_indices), NB pages in flight.  Every load is
+  // unconditional -- past the group's end it goes through a size-0
+  // descriptor -- and the only branches around code are VMEM-free (the tail
+  // consumes), so the compiler's wait before consuming a page is exactly
+  // "NB-1 pages still outstanding".
+  Regs buf[T::NB];
+  int g_start = 0, gsize = min(npg, kInlinePages);
+  while (true) {
 #pragma unroll
-    for (int i = 0; i < T::NBUF - 1; ++i) load_page(buf[i], mi::read_lane_i(pid, min(i, cnt - 1)));
+    for (int s = 0; s < T::NB; ++s) issue(buf[s], s, gsize);
+    auto page_valid = [&](int k) {
+      const int valid = (g_start + k == npg - 1) ? last_valid : kPageSize;
+      return page_ok(k, page_id(k), gsize) ? valid : 0;
+    };
+    const int full = gsize / T::NB;
+    for (int it = 0; it < full; ++it) {
 #pragma unroll
-    for (int i = 0; i < kInlinePages; ++i) {
-      if (i >= cnt) break;
-      load_page(buf[(i + T::NBUF - 1) % T::NBUF], mi::read_lane_i(pid, min(i + T::NBUF - 1, cnt - 1)));
-      const int page = mi::read_lane_i(pid, i);
-      int valid = (g0 + i == npg - 1) ? last_valid : kPageSize;
-      if (page < 0 || page >= p.num_pages) valid = 0;
-      consume(buf[i % T::NBUF], valid);
+      for (int s = 0; s < T::NB; ++s) {
+        const int k = it * T::NB + s;
+        consume(buf[s], page_valid(k));
+        issue(buf[s], k + T::NB, gsize);
+      }
     }
+    const int rem = gsize - full * T::NB;
+#pragma unroll
+    for (int s = 0; s < T::NB - 1; ++s)
+      if (s < rem) consume(buf[s], page_valid(full * T::NB + s));
+    g_start += gsize;
+    if (g_start >= npg) break;
+    gsize = min(64, npg - g_start);
+    pidv = (lane < gsize) ? p.indices[page_begin + g_start + lane] : -1;
+    // Wait here, while only size-0 loads are outstanding, so the loop head
+    // carries no pending load (the first group's Q loads stay in flight).
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   }
 
   // ---- per-head denominators; O rows are heads 4g + i
-  float lt = l_run + mi::lane_shuffle(l_run, lane ^ 16);
-  lt += mi::lane_shuffle(lt, lane ^ 32);
-  float lo[4], mo[4];
+  float lt = sum_xor16(l_run);
+  lt = sum_xor32(lt);
+  float lo[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    lo[i] = mi::lane_shuffle(lt, 4 * g + i);
-    mo[i] = mi::lane_shuffle(m_run, 4 * g + i);
-  }
-  (void)mo;
+  for (int i = 0; i < 4; ++i) lo[i] = mi::lane_shuffle(lt, 4 * g + i);
 
   if (nsplit == 1) {
 #pragma unroll
@@ -484,6 +577,8 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, lds_t* ld
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 
   // Online merge over the splits, 64 per round (lane s holds split s's m, l).
+  // The m / l loads and the first KB splits' partial rows are issued
+  // together, so a merge of up to KB splits costs one round trip.
   float M[G], Lt[G], sum[G][T::OUT];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
@@ -492,50 +587,50 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, lds_t* ld
 #pragma unroll
     for (int k = 0; k < T::OUT; ++k) sum[h][k] = 0.f;
   }
+  auto load_rows = [&](float (&v)[T::KB][G][T::OUT], int r0, int s0, int nr) {
+#pragma unroll
+    for (int q = 0; q < T::KB; ++q) {
+      const int s = r0 + min(s0 + q, nr - 1);
+      const float* src = p.po + int64_t((item_base + s) * p.hkv + hkv) * G * D;
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int k = 0; k < T::OUT; ++k) v[q][h][k] = coherent_load(src + h * D + lane + 64 * k);
+    }
+  };
   for (int r0 = 0; r0 < nsplit; r0 += 64) {
     const int nr = min(64, nsplit - r0);
-    const int my_unit = (item_base + r0 + lane) * p.hkv + hkv;
+    const int my_unit = (item_base + r0 + min(lane, nr - 1)) * p.hkv + hkv;
     float ms[G], ls[G], wgt[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      ms[h] = -INFINITY;
-      ls[h] = 0.f;
-      if (lane < nr) {
-        ms[h] = coherent_load(p.pml + (int64_t(my_unit) * G + h) * 2 + 0);
-        ls[h] = coherent_load(p.pml + (int64_t(my_unit) * G + h) * 2 + 1);
-      }
+      ms[h] = coherent_load(p.pml + (int64_t(my_unit) * G + h) * 2 + 0);
+      ls[h] = coherent_load(p.pml + (int64_t(my_unit) * G + h) * 2 + 1);
     }
+    float v[T::KB][G][T::OUT];
+    load_rows(v, r0, 0, nr);
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      const float Mn = fmaxf(M[h], mi::wave_max(ms[h]));
+      if (lane >= nr) ms[h] = -INFINITY;
+      const float Mn = fmaxf(M[h], wave_max_fast(ms[h]));
       const float f = (M[h] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M[h] - Mn);
       Lt[h] *= f;
 #pragma unroll
       for (int k = 0; k < T::OUT; ++k) sum[h][k] *= f;
-      wgt[h] = (lane < nr && ms[h] != -INFINITY) ? __builtin_amdgcn_exp2f(ms[h] - Mn) : 0.f;
-      Lt[h] += mi::wave_sum(wgt[h] * ls[h]);
+      wgt[h] = (ms[h] != -INFINITY) ? __builtin_amdgcn_exp2f(ms[h] - Mn) : 0.f;
+      Lt[h] += wave_sum_fast(wgt[h] * ls[h]);
       M[h] = Mn;
     }
-    constexpr int kBatch = 4;  // splits whose partials are in flight together
-    for (int s0 = 0; s0 < nr; s0 += kBatch) {
-      float v[kBatch][G][T::OUT];
+    for (int s0 = 0; s0 < nr; s0 += T::KB) {
+      if (s0 > 0) load_rows(v, r0, s0, nr);
 #pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const int s = r0 + min(s0 + j, nr - 1);
-        const float* src = p.po + int64_t((item_base + s) * p.hkv + hkv) * G * D;
-#pragma unroll
-        for (int h = 0; h < G; ++h)
-#pragma unroll
-          for (int k = 0; k < T::OUT; ++k) v[j][h][k] = coherent_load(src + h * D + lane + 64 * k);
-      }
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        if (s0 + j >= nr) break;
+      for (int q = 0; q < T::KB; ++q) {
+        if (s0 + q >= nr) break;
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-          const float ws = mi::read_lane(wgt[h], s0 + j);
+          const float ws = mi::read_lane(wgt[h], s0 + q);
 #pragma unroll
-          for (int k = 0; k < T::OUT; ++k) sum[h][k] += ws * v[j][h][k];
+          for (int k = 0; k < T::OUT; ++k) sum[h][k] += ws * v[q][h][k];
         }
       }
     }
@@ -550,16 +645,23 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, lds_t* ld
   if (lane == 0) coherent_store(counter, 0);
 }
 
-// head_dim <= 128: registers capped at 256 per wave (double-buffered pages
-// need ~160-200), so at least two waves share a SIMD; measured faster than a
-// deeper per-wave prefetch at lower occupancy.  head_dim 256 needs the full
-// register file for two pages in flight.
+// head_dim <= 128: registers capped at 256 per wave, so at least two waves
+// share a SIMD (8 units per CU).  head_dim 256 needs the full register file.
 template <int D, int G>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void decode_run_kernel(RunParams p) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(D <= 128 ? MI_DECODE_WAVES : 1))) void decode_run_kernel(
+    RunParams p) {
   __shared__ __attribute__((aligned(16))) char slot[DecodeTraits<D, G>::SLOT];
   lds_t* lds = (lds_t*)slot;
+  int u = blockIdx.x;
+  // The first item is read before the unit count is known (in bounds either
+  // way), so the two reads are in flight together.
+  int iv = load_item_word(p, u);
   const int num_units = p.header->num_units;
-  for (int u = blockIdx.x; u < num_units; u += gridDim.x) decode_unit<D, G>(p, u, lds);
+  while (u < num_units) {
+    decode_unit<D, G>(p, u, iv, lds);
+    u += gridDim.x;
+    if (u < num_units) iv = load_item_word(p, u);
+  }
 }
 
 typedef void (*RunKernel)(RunParams);
@@ -671,13 +773,14 @@ extern "C" int mi_decode_run(void* workspace, size_t workspace_bytes, const void
   rp.q = static_cast<const uint16_t*>(q);
   rp.q_sb = q_stride_batch;
   rp.q_sh = q_stride_head;
-  rp.pool = static_cast<const uint16_t*>(paged_kv_cache);
+  rp.pool = static_cast<const char*>(paged_kv_cache);
   rp.num_pages = num_pages;
   rp.indices = kv_indices;
   rp.out = static_cast<uint16_t*>(out);
   rp.o_sb = out_stride_batch;
   rp.o_sh = out_stride_head;
   rp.hkv = num_kv_heads;
+  rp.max_items = L.max_items;
   const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf(float(head_dim));
   rp.scale_log2 = scale * mi::kLog2e;
   RunKernel k = pick_kernel(head_dim, num_qo_heads / num_kv_heads);
