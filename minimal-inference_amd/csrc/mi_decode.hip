@@ -6,23 +6,23 @@
 // (model.py:286-295 restates it with repeat_interleave + SDPA).
 //
 // Work decomposition.  plan() cuts every request's page list into `nsplit`
-// contiguous page ranges ("items") so that items x kv_heads ("units") is close
-// to kUnitsPerCU units per CU, and copies the first kInlinePages page ids of
-// each item into the item so a wave can start its page loads right after
-// reading the item.  One 64-lane wave runs one unit: it streams the unit's K
-// and V pages for one KV head and serves all `group` Q heads of that KV head,
-// so each KV byte is read from HBM once per step.
+// contiguous page ranges ("items") so that items x kv_heads ("units") fill
+// one resident round of kUnitsPerCU waves per CU, and copies the first
+// kInlinePages page ids of each item into the item, so a wave starts its page
+// loads right after reading the item.  One 64-lane wave runs one unit: it
+// streams the unit's K and V pages for one KV head and serves all `group` Q
+// heads of that KV head, so each KV byte is read from HBM once per step.
 //
 // Per 16-token page, one wave:
-//   * S = Q K^T with 16x16x32 bf16 MFMAs: Q rows are the group's heads
-//     (zero-padded to 16), K columns are the page's tokens, and each lane's
-//     16-byte global load of K is directly its B operand;
+//   * loads K and V through a per-page buffer descriptor (size 0 for an
+//     invalid or absent page: the loads return zeros and touch no memory),
+//     NB pages in flight, and stages them in LDS;
+//   * S^T = K Q^T with 16x16x32 bf16 MFMAs (Q columns are the group's heads,
+//     zero-padded to 16);
 //   * online softmax in the exp2 domain with a lazy running max (rescale only
 //     when the max grows by more than 2^8, so rescales are rare);
-//   * O += P V on the VALU: lane (t, c) holds 16 head_dim values of token t
-//     and accumulates them for all group heads; P reaches it by ds_bpermute.
-// Pages are triple-buffered in registers (two pages in flight while one is
-// consumed).  At the end the per-token partial sums are reduced through LDS.
+//   * O += P V with 16x16x16 bf16 MFMAs: the S^T accumulator is already the P
+//     operand, V comes from the gfx950 LDS transpose read.
 //
 // Split merge without cache flushes.  Units of a request with several splits
 // write (O, m, l) partials with device-coherent (sc1, write-through) stores,
