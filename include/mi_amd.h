@@ -67,6 +67,30 @@ int mi_paged_kv_append(const void* append_key, int64_t key_stride_token, int64_t
                        int32_t head_dim, int32_t page_size, mi_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
+ * Fused rotate-half RoPE + paged KV append.
+ * Replaces, per layer, apply_rotary_emb on q and k (model.py:92-107, called
+ * at model.py:169-170) followed by the append of model.py:203-216.
+ *
+ * qkv: [num_tokens] rows of bf16, row stride qkv_stride_token elements; each
+ * row holds num_qo_heads q heads, then num_kv_heads k heads, then
+ * num_kv_heads v heads, head_dim contiguous each.  Token i is rotated with
+ * row rope_positions[i] (clamped to [0, table_rows)) of cos_table / sin_table
+ * ([table_rows][head_dim] bf16, the rotate-half layout of model.py:79-89):
+ * out = bf16(bf16(x * cos) + bf16(rotate_half(x) * sin)), bit-identical to
+ * the reference's bf16 torch ops.  Rotated q goes to q_out (element strides;
+ * it may alias qkv's q columns); rotated k and the v row are appended with
+ * the placement rule of mi_paged_kv_append.  head_dim: multiple of 16.
+ * ------------------------------------------------------------------------ */
+int mi_rope_append(const void* qkv, int64_t qkv_stride_token, const int32_t* rope_positions,
+                   const void* cos_table, const void* sin_table, int64_t table_rows, void* q_out,
+                   int64_t q_out_stride_token, int64_t q_out_stride_head,
+                   const int32_t* batch_indices, const int32_t* positions, int64_t num_tokens,
+                   void* paged_kv_cache, int64_t num_pages, const int32_t* kv_indices,
+                   const int32_t* kv_indptr, const int32_t* kv_last_page_len, int32_t batch_size,
+                   int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                   mi_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
  * Split-K paged decode attention.
  * Replaces flashinfer.decode.BatchDecodeWithPagedKVCacheWrapper:
  *   plan  -- scheduler.py:402-413, 905-916, 927-938

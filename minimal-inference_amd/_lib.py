@@ -38,6 +38,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _vp, _c_i64, _vp, _vp, _vp,
          _c_i32, _c_i32, _c_i32, _c_i32, _vp],
     ),
+    "mi_rope_append": (
+        ctypes.c_int,
+        [_vp, _c_i64, _vp, _vp, _vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _vp, _c_i64, _vp, _vp,
+         _vp, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp],
+    ),
     "mi_decode_workspace_size": (_c_sz, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "mi_decode_plan": (
         ctypes.c_int,

@@ -54,6 +54,124 @@ __global__ __launch_bounds__(256) void append_kernel(AppendParams p) {
   }
 }
 
+// ------------------------------------------------------------ RoPE + append
+// Rotate-half RoPE on the fused qkv rows, then the K/V append, in one pass.
+//
+// Replaces, per layer, the reference's apply_rotary_emb on q and k
+// (model.py:92-107, called at model.py:169-170) followed by the append
+// (model.py:203-216).  The arithmetic is the reference's bf16 composition
+// x * cos + rotate_half(x) * sin with cos / sin already in bf16
+// (server.py:251): each product is exact in fp32 and rounded to bf16, their
+// sum is taken in fp32 and rounded to bf16 -- what the three bf16 torch ops
+// do -- so the result is bit-identical to the unfused ops.
+//
+// Work units per token: (H_q + H_kv) heads x D/16 rotate units (8 pairs
+// (j, j + D/2) each: one 16-byte load from each half) and H_kv x D/8 copy
+// units for V.  Q is written to q_out (may alias qkv's q columns: every unit
+// reads both of its halves before writing them); rotated K and V go to the
+// token's page slot with the same placement rule as append_kernel.
+struct RopeAppendParams {
+  const uint16_t* qkv;
+  int64_t qkv_stride;  // elements between tokens; q heads, k heads, v heads contiguous
+  const int32_t* rope_pos;
+  const uint16_t* cos;
+  const uint16_t* sin;
+  int64_t table_rows;
+  uint16_t* q_out;
+  int64_t qo_stride_tok, qo_stride_head;
+  const int32_t* batch_indices;
+  const int32_t* positions;
+  int64_t num_tokens;
+  uint16_t* pool;
+  int64_t num_pages;
+  const int32_t* indices;
+  const int32_t* indptr;
+  int32_t batch_size, num_qo_heads, num_kv_heads, head_dim, page_size;
+};
+
+// bf16(a * b) with the product exact in fp32 (8-bit x 8-bit mantissas).
+__device__ __forceinline__ float bf16_mul(float a, float b) { return mi::bf16_to_f32(mi::f32_to_bf16(a * b)); }
+
+__device__ __forceinline__ float lo16(uint32_t w) { return mi::bf16_lo(w); }
+__device__ __forceinline__ float hi16(uint32_t w) { return mi::bf16_hi(w); }
+
+// out_lo = x1 * c1 + (-x2) * s1, out_hi = x2 * c2 + x1 * s2, 8 lanes each
+__device__ __forceinline__ void rope8(uint4 x1, uint4 x2, uint4 c1, uint4 s1, uint4 c2, uint4 s2, uint4& o1,
+                                      uint4& o2) {
+  const uint32_t* a = &x1.x;
+  const uint32_t* b = &x2.x;
+  const uint32_t* ca = &c1.x;
+  const uint32_t* sa = &s1.x;
+  const uint32_t* cb = &c2.x;
+  const uint32_t* sb = &s2.x;
+  uint32_t* oa = &o1.x;
+  uint32_t* ob = &o2.x;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    float r0, r1;
+    r0 = bf16_mul(lo16(a[w]), lo16(ca[w])) + bf16_mul(-lo16(b[w]), lo16(sa[w]));
+    r1 = bf16_mul(hi16(a[w]), hi16(ca[w])) + bf16_mul(-hi16(b[w]), hi16(sa[w]));
+    oa[w] = mi::pack_bf16x2(r0, r1);
+    r0 = bf16_mul(lo16(b[w]), lo16(cb[w])) + bf16_mul(lo16(a[w]), lo16(sb[w]));
+    r1 = bf16_mul(hi16(b[w]), hi16(cb[w])) + bf16_mul(hi16(a[w]), hi16(sb[w]));
+    ob[w] = mi::pack_bf16x2(r0, r1);
+  }
+}
+
+__global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams p) {
+  const int d = p.head_dim, half = d >> 1;
+  const int rot_units = (p.num_qo_heads + p.num_kv_heads) * (d >> 4);
+  const int per_token = rot_units + p.num_kv_heads * (d >> 3);
+  const int64_t total = p.num_tokens * per_token;
+  const int64_t tok_stride = int64_t(p.num_kv_heads) * d;
+  const int64_t kv_stride = int64_t(p.page_size) * tok_stride;
+  const int64_t page_stride = 2 * kv_stride;
+  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t i = idx / per_token;
+    const int r = int(idx - i * per_token);
+    const uint16_t* row = p.qkv + i * p.qkv_stride;
+    // page slot of token i (K and V units only)
+    auto slot_ptr = [&](int kh) -> uint16_t* {
+      const int b = p.batch_indices[i];
+      const int pos = p.positions[i];
+      if (b < 0 || b >= p.batch_size || pos < 0) return nullptr;
+      const int64_t it = int64_t(p.indptr[b]) + pos / p.page_size;
+      if (it >= p.indptr[b + 1]) return nullptr;
+      const int64_t page = p.indices[it];
+      if (page < 0 || page >= p.num_pages) return nullptr;
+      return p.pool + page * page_stride + (pos % p.page_size) * tok_stride + int64_t(kh) * d;
+    };
+    if (r < rot_units) {
+      const int h = r / (d >> 4);
+      const int c = (r - h * (d >> 4)) * 8;
+      int rp = p.rope_pos[i];
+      rp = rp < 0 ? 0 : (rp >= p.table_rows ? int(p.table_rows - 1) : rp);
+      const uint16_t* cs = p.cos + int64_t(rp) * d;
+      const uint16_t* sn = p.sin + int64_t(rp) * d;
+      const uint16_t* src = row + int64_t(h) * d;
+      uint4 o1, o2;
+      rope8(mi::load16(src + c), mi::load16(src + half + c), mi::load16(cs + c), mi::load16(sn + c),
+            mi::load16(cs + half + c), mi::load16(sn + half + c), o1, o2);
+      if (h < p.num_qo_heads) {
+        uint16_t* dst = p.q_out + i * p.qo_stride_tok + int64_t(h) * p.qo_stride_head;
+        mi::store16(dst + c, o1);
+        mi::store16(dst + half + c, o2);
+      } else if (uint16_t* dst = slot_ptr(h - p.num_qo_heads)) {
+        mi::store16(dst + c, o1);
+        mi::store16(dst + half + c, o2);
+      }
+    } else {
+      const int u = r - rot_units;
+      const int kh = u / (d >> 3);
+      const int c = (u - kh * (d >> 3)) * 8;
+      if (uint16_t* dst = slot_ptr(kh))
+        mi::store16(dst + kv_stride + c,
+                    mi::load16(row + int64_t(p.num_qo_heads + p.num_kv_heads + kh) * d + c));
+    }
+  }
+}
+
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
 }  // namespace
@@ -108,4 +226,64 @@ extern "C" int mi_paged_kv_append(const void* append_key, int64_t key_stride_tok
   hipLaunchKernelGGL(append_kernel, dim3(unsigned(blocks)), dim3(threads), 0,
                      static_cast<hipStream_t>(stream), p);
   return mi::check_launch("append_kernel");
+}
+
+extern "C" int mi_rope_append(const void* qkv, int64_t qkv_stride_token, const int32_t* rope_positions,
+                              const void* cos_table, const void* sin_table, int64_t table_rows, void* q_out,
+                              int64_t q_out_stride_token, int64_t q_out_stride_head,
+                              const int32_t* batch_indices, const int32_t* positions, int64_t num_tokens,
+                              void* paged_kv_cache, int64_t num_pages, const int32_t* kv_indices,
+                              const int32_t* kv_indptr, const int32_t* kv_last_page_len, int32_t batch_size,
+                              int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                              mi_stream_t stream) {
+  (void)kv_last_page_len;  // slot placement depends on positions only
+  mi::clear_error();
+  if (num_tokens < 0 || batch_size < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || num_pages <= 0 ||
+      table_rows <= 0)
+    return mi::fail(MI_ERR_INVALID, "rope_append: bad sizes (tokens=%lld batch=%d heads=%d/%d pages=%lld rows=%lld)",
+                    (long long)num_tokens, batch_size, num_qo_heads, num_kv_heads, (long long)num_pages,
+                    (long long)table_rows);
+  if (head_dim <= 0 || head_dim % 16 != 0)
+    return mi::fail(MI_ERR_UNSUPPORTED, "rope_append: head_dim %d must be a positive multiple of 16", head_dim);
+  if (page_size <= 0) return mi::fail(MI_ERR_INVALID, "rope_append: page_size %d", page_size);
+  if (num_tokens == 0) return MI_OK;
+  if (!qkv || !rope_positions || !cos_table || !sin_table || !q_out || !batch_indices || !positions ||
+      !paged_kv_cache || !kv_indices || !kv_indptr)
+    return mi::fail(MI_ERR_INVALID, "rope_append: null pointer argument");
+  if (!aligned16(qkv) || !aligned16(cos_table) || !aligned16(sin_table) || !aligned16(q_out) ||
+      !aligned16(paged_kv_cache) || qkv_stride_token % 8 || q_out_stride_token % 8 || q_out_stride_head % 8)
+    return mi::fail(MI_ERR_INVALID, "rope_append: qkv / q_out rows, tables and pool must be 16-byte aligned");
+  if (qkv_stride_token < int64_t(num_qo_heads + 2 * num_kv_heads) * head_dim)
+    return mi::fail(MI_ERR_INVALID, "rope_append: qkv row stride %lld shorter than (Hq + 2 Hkv) * D",
+                    (long long)qkv_stride_token);
+  RopeAppendParams p{static_cast<const uint16_t*>(qkv),
+                     qkv_stride_token,
+                     rope_positions,
+                     static_cast<const uint16_t*>(cos_table),
+                     static_cast<const uint16_t*>(sin_table),
+                     table_rows,
+                     static_cast<uint16_t*>(q_out),
+                     q_out_stride_token,
+                     q_out_stride_head,
+                     batch_indices,
+                     positions,
+                     num_tokens,
+                     static_cast<uint16_t*>(paged_kv_cache),
+                     num_pages,
+                     kv_indices,
+                     kv_indptr,
+                     batch_size,
+                     num_qo_heads,
+                     num_kv_heads,
+                     head_dim,
+                     page_size};
+  const int64_t per_token = int64_t(num_qo_heads + num_kv_heads) * (head_dim / 16) + int64_t(num_kv_heads) * (head_dim / 8);
+  const int64_t work = num_tokens * per_token;
+  const int threads = 256;
+  int64_t blocks = (work + threads - 1) / threads;
+  const int64_t cap = int64_t(mi::num_cus()) * 16;
+  if (blocks > cap) blocks = cap;
+  hipLaunchKernelGGL(rope_append_kernel, dim3(unsigned(blocks)), dim3(threads), 0,
+                     static_cast<hipStream_t>(stream), p);
+  return mi::check_launch("rope_append_kernel");
 }

@@ -47,4 +47,4 @@ int num_cus() {
 
 extern "C" const char* mi_last_error(void) { return g_last_error; }
 
-extern "C" int mi_version(void) { return 100; }
+extern "C" int mi_version(void) { return 200; }

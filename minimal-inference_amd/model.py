@@ -10,7 +10,10 @@ integer GQA group runs natively.
 
 Layout choices (dense path only; numerics match the separate-projection
 form): q/k/v projections are one fused GEMM and gate/up one fused GEMM, and
-prefill computes logits only for each request's last position.  RoPE tables
+prefill computes logits only for each request's last position.  By default
+RoPE on q and k and the K/V append run as one HIP launch
+(``rope_append_paged_kv_cache``), bit-identical to the reference's bf16
+RoPE ops followed by the append; ``fused_rope=False`` keeps the separate ops.  RoPE tables
 are held in the model dtype, as the reference's are after ``.to(dtype)``
 (server.py:251).  Weights are random-initialised on the device (N(0, 0.02),
 norms 1) -- the benchmark configurations use random weights.
@@ -26,7 +29,7 @@ import os
 import torch
 import torch.nn.functional as F
 
-from .page import append_paged_kv_cache
+from .page import append_paged_kv_cache, rope_append_paged_kv_cache
 
 
 @dataclasses.dataclass
@@ -148,8 +151,10 @@ class AttentionBackend:
 
 
 class Model:
-    def __init__(self, cfg: ModelConfig, device, dtype=torch.bfloat16, seed: int = 0, max_positions: int | None = None):
+    def __init__(self, cfg: ModelConfig, device, dtype=torch.bfloat16, seed: int = 0, max_positions: int | None = None,
+                 fused_rope: bool = True):
         self.cfg = cfg
+        self.fused_rope = fused_rope
         self.device = torch.device(device)
         self.dtype = dtype
         gen = torch.Generator(device=self.device).manual_seed(seed)
@@ -182,22 +187,30 @@ class Model:
         cfg = self.cfg
         nq, nkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
         x = F.embedding(input_ids, self.embed)
-        cos = self.cos.index_select(0, positions)
-        sin = self.sin.index_select(0, positions)
+        fused = self.fused_rope
+        if fused:
+            rope_pos = positions if positions.dtype == torch.int32 else positions.to(torch.int32)
+        else:
+            cos = self.cos.index_select(0, positions)
+            sin = self.sin.index_select(0, positions)
         t = input_ids.shape[0]
         backend._layer_idx = 0
         for L in self.layers:
             layer_idx = backend.next_layer()
             h = F.rms_norm(x, (cfg.hidden_size,), L.in_norm, cfg.rms_norm_eps)
             qkv = F.linear(h, L.w_qkv, L.b_qkv)
-            q = qkv[:, : nq * d].view(t, nq, d)
-            k = qkv[:, nq * d: (nq + nkv) * d].view(t, nkv, d)
-            v = qkv[:, (nq + nkv) * d:].view(t, nkv, d)
-            q = apply_rope(q, cos, sin)
-            k = apply_rope(k, cos, sin)
             kv_data = backend.paged_kv_cache.kv_data[layer_idx]
-            append_paged_kv_cache(k, v, backend.batch_indices, backend.positions, kv_data,
-                                  backend.kv_page_indices, backend.kv_page_indptr, backend.kv_last_page_len)
+            if fused:
+                # q rotated in place in qkv's q columns; k rotated and v appended
+                q = rope_append_paged_kv_cache(qkv, nq, nkv, rope_pos, self.cos, self.sin, backend.batch_indices,
+                                               backend.positions, kv_data, backend.kv_page_indices,
+                                               backend.kv_page_indptr, backend.kv_last_page_len)
+            else:
+                q = apply_rope(qkv[:, : nq * d].view(t, nq, d), cos, sin)
+                k = apply_rope(qkv[:, nq * d: (nq + nkv) * d].view(t, nkv, d), cos, sin)
+                v = qkv[:, (nq + nkv) * d:].view(t, nkv, d)
+                append_paged_kv_cache(k, v, backend.batch_indices, backend.positions, kv_data,
+                                      backend.kv_page_indices, backend.kv_page_indptr, backend.kv_last_page_len)
             o = backend.wrapper.run(q, kv_data)
             x = x + F.linear(o.view(t, nq * d), L.w_o)
             h = F.rms_norm(x, (cfg.hidden_size,), L.post_norm, cfg.rms_norm_eps)

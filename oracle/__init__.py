@@ -12,6 +12,8 @@ Modules:
   attention  -- gather-based paged decode and causal prefill attention in fp32.
   sampling   -- greedy argmax, bf16 temperature quantisation, the fp32
                 (top-p restricted) sampling distribution.
+  rope       -- rotate-half RoPE tables and the bf16 op sequence of the
+                reference, and the unfused RoPE-then-append sequence.
 
 Pinning status per function is recorded in each module's docstring.
 """
