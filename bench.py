@@ -28,6 +28,13 @@ workload (same model, batch and mean context); otherwise null.
 
 ``cpu_baseline`` times the CPU oracle's gather-based attention on one layer of
 the same batch.
+
+``path_kernels`` times the other kernels of the path on the same state, each
+as repeated launches captured in one hipGraph and replayed between HIP events: the ragged
+causal prefill attention of the 32 prompts for one layer (MFMA bound:
+flops = sum_b 4 * H_q * D * L_b (L_b + 1) / 2, against 2.5 PFLOP/s bf16), the
+decode-step fused RoPE + KV append and the sampler for the 32 rows
+(latency bound: microseconds), and the device page-table step.
 """
 
 from __future__ import annotations
@@ -51,6 +58,77 @@ PUBLISHED_TOKS = 1532.0  # reference README.md:56, H100, 32 concurrent, aggregat
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_us(fn, iters: int) -> float:
+    """Average GPU microseconds per call of ``fn``: ``iters`` calls captured in
+    one hipGraph (so host launch cost is excluded), replayed between HIP
+    events on the current stream after warm-up calls on a side stream."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(iters):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    graph.replay()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1000 / iters
+
+
+def path_kernel_times(sch, cfg, reqs, lens, dev) -> dict:
+    """The path's other kernels on the bench's real state (see module doc)."""
+    import torch
+
+    from minimal_inference_amd.page import rope_append_paged_kv_cache
+    from minimal_inference_amd.prefill import BatchPrefillWithPagedKVCacheWrapper
+
+    B = len(reqs)
+    hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    res = {}
+    # ragged causal prefill over the prompts' own pages (first ceil(L/16) pages of each request)
+    ip = sch.d_indptr[: B + 1].cpu().tolist()
+    ix = sch.d_indices[: ip[-1]].cpu()
+    pages = [ix[ip[b]: ip[b] + math.ceil(lens[b] / 16)] for b in range(B)]
+    p_indptr = torch.tensor([0] + list(torch.tensor([len(x) for x in pages]).cumsum(0).tolist()),
+                            dtype=torch.int32, device=dev)
+    p_indices = torch.cat(pages).to(dev)
+    p_last = torch.tensor([n - (math.ceil(n / 16) - 1) * 16 for n in lens], dtype=torch.int32, device=dev)
+    qo = torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()), dtype=torch.int32, device=dev)
+    total = sum(lens)
+    q = torch.randn(total, hq, d, device=dev, dtype=torch.bfloat16)
+    ws = torch.empty(128 << 20, dtype=torch.uint8, device=dev)
+    pw = BatchPrefillWithPagedKVCacheWrapper(ws)
+    pw.plan(qo, p_indptr, p_indices, p_last, hq, hkv, d, 16, causal=True, max_total_q=total)
+    out = torch.empty_like(q)
+    us = time_us(lambda: pw.run(q, sch.kv.kv_data[0], out=out), 20)
+    flops = sum(4 * hq * d * (L * (L + 1) // 2) for L in lens)
+    res["prefill_attn"] = {"us": round(us, 2), "tflops": round(flops / us / 1e6, 1),
+                           "frac_of_2500": round(flops / us / 1e6 / 2500, 4), "query_rows": total}
+    # decode-step fused RoPE + append for the batch's rows (writes the next position's slot)
+    qkv = torch.randn(B, (hq + 2 * hkv) * d, device=dev, dtype=torch.bfloat16)
+    model = sch.model
+    us = time_us(lambda: rope_append_paged_kv_cache(qkv, hq, hkv, sch.d_pos[:B], model.cos, model.sin,
+                                                    sch.d_batch[:B], sch.d_pos[:B], sch.kv.kv_data[0],
+                                                    sch.d_indices, sch.d_indptr[: B + 1], sch.d_last[:B]), 200)
+    res["rope_append_decode"] = {"us": round(us, 2), "rows": B}
+    # sampler: the batch's settings (half greedy, half T=0.7 / top-p 0.9)
+    logits = torch.randn(B, cfg.vocab_size, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    smp = sch.sampler
+    smp.set_params([r.temperature for r in reqs], [r.top_p for r in reqs])
+    us = time_us(lambda: smp.sample(logits, B), 100)
+    res["sampler"] = {"us": round(us, 2), "rows": B, "vocab": cfg.vocab_size}
+    return res
 
 
 def measured_traffic(model: str, batch: int, mean_context: float):
@@ -184,6 +262,9 @@ def main() -> int:
     log(f"decode attention: {attn_us:.2f} us/launch, {achieved:.0f} GB/s "
         f"({100 * achieved / PEAK_HBM_GBPS:.1f}% of {PEAK_HBM_GBPS:.0f}), {alg_bytes / 1e6:.1f} MB/launch")
 
+    path = path_kernel_times(sch, cfg, reqs, lens, dev)
+    log(f"path kernels: {path}")
+
     # ---------------- CPU baseline: the oracle on one layer of the same batch
     cpu = None
     if not args.no_cpu_baseline:
@@ -239,6 +320,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic},
         "cpu_baseline": cpu,
+        "path_kernels": path,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -138,13 +138,17 @@ int mi_decode_run(void* workspace, size_t workspace_bytes, const void* q, int64_
  * qo_indptr[b] .. qo_indptr[b+1].  With causal != 0, query row i of request b
  * attends to KV tokens j <= i + (kv_len_b - qo_len_b) (bottom-right aligned).
  * total_q must be >= qo_indptr[batch_size]; it sizes the launch on the host.
- * head_dim in {64, 128}; page_size == 16.
+ * plan() takes the head counts and head_dim (as FlashInfer's plan does): a
+ * workgroup serves all num_qo_heads / num_kv_heads (1..8) Q heads of one KV
+ * head, and the query positions per workgroup depend on both.
+ * head_dim in {64, 128, 256}; page_size == 16.
  * ------------------------------------------------------------------------ */
 size_t mi_prefill_workspace_size(int32_t batch_size, int64_t total_q);
 
 int mi_prefill_plan(void* workspace, size_t workspace_bytes, const int32_t* qo_indptr,
                     const int32_t* kv_indptr, const int32_t* kv_last_page_len, int32_t batch_size,
-                    int64_t total_q, int32_t page_size, mi_stream_t stream);
+                    int64_t total_q, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                    int32_t page_size, mi_stream_t stream);
 
 int mi_prefill_run(void* workspace, size_t workspace_bytes, const void* q, int64_t q_stride_token,
                    int64_t q_stride_head, const void* paged_kv_cache, int64_t num_pages,

@@ -56,7 +56,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mi_prefill_workspace_size": (_c_sz, [_c_i32, _c_i64]),
     "mi_prefill_plan": (
         ctypes.c_int,
-        [_vp, _c_sz, _vp, _vp, _vp, _c_i32, _c_i64, _c_i32, _vp],
+        [_vp, _c_sz, _vp, _vp, _vp, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _vp],
     ),
     "mi_prefill_run": (
         ctypes.c_int,

@@ -5,20 +5,30 @@
 // (model.py:235, mode == "prefill").  Query row i of request b sees KV tokens
 // j <= i + (kv_len - qo_len); the reference always has kv_len == qo_len.
 //
-// plan() (one workgroup) lists 64-row query tiles of every request, the
-// heaviest (last) tile of a request first.  run() launches (tiles, q_heads)
-// workgroups of four waves; wave w owns query rows 16w..16w+15 of the tile.
-// Per 32-token KV tile:
-//   S^T = K Q^T  -- 16x16x32 MFMAs; K rows come straight from the pool with
-//                   16-byte loads, Q^T is held in registers;
-//   online softmax per query row in the exp2 domain;
-//   O += P V     -- the S^T accumulator layout is reused as the P operand
-//                   (each lane already holds 8 keys of one query row); V is
-//                   staged transposed in LDS by the workgroup so every lane
-//                   reads its 8 keys of one head_dim column as two 8-byte
-//                   LDS reads.
-// Waves whose rows are causally finished skip the MFMAs of a tile but keep
-// the workgroup barriers.
+// Work decomposition.  A workgroup (4 waves) owns `bm` query positions of one
+// request and ALL `group` Q heads of one KV head: (bm / 16) x group row blocks
+// of 16 (position, head) rows, dealt to the waves round robin (at most two per
+// wave, computed together so every K / V operand read from LDS feeds both).
+// bm = 128 / group rounded down to a multiple of 16 (at least 16; 64 / group
+// for head_dim 256), so a workgroup covers 80-128 rows and every K/V byte it
+// stages serves all the heads of its group.  plan() lists the tiles request
+// by request (longest prompt first), each request's tiles heaviest first; the
+// grid maps tile-major, so the XCD that a KV head's workgroups land on runs
+// one request's tiles back to back and finds its K / V in L2.
+//
+// Per 64-key tile: the workgroup stages K and V in LDS (double buffered: the
+// next tile's global loads are in flight while this one is consumed; one
+// barrier per tile); each wave, per row block:
+//   S^T = K Q^T  -- 16x16x32 MFMAs, K rows read from LDS as the A operand,
+//                   Q^T held in registers as B; lane (g, n) gets
+//                   S^T[key 4g+i][row n] for each 16-key block;
+//   online softmax per row in the exp2 domain with a lazy running max
+//   (rescale only when the max grows by more than 2^8); row maxima across
+//   lane groups with the gfx950 lane-swap instructions;
+//   O += P V     -- 16x16x32 MFMAs over 32 keys: the S^T accumulators of two
+//                   key blocks are exactly the P operand (lane (g, n) holds
+//                   keys {4g+i} of both), and V comes from the gfx950 LDS
+//                   transpose read in the same key order.
 #include <math.h>
 
 #include "mi_common.h"
@@ -26,16 +36,20 @@
 namespace {
 
 constexpr int kPageSize = 16;
-constexpr int kTileRows = 64;
-constexpr int kKvTile = 32;
+constexpr int kMinRows = 16;   // smallest query-position block per workgroup
+constexpr int kKvTile = 64;    // keys per staged tile (4 pages)
+constexpr float kLazyRescale = 8.0f;
+#ifndef PREFILL_WAVES
+#define PREFILL_WAVES 2
+#endif
 
 struct alignas(32) PrefillTile {
   int b;
   int q_begin;  // absolute first query row of the tile
-  int q_rows;   // rows in this tile (<= 64)
+  int q_rows;   // positions in this tile (<= bm)
   int qo_len;
   int kv_len;
-  int row0;           // first row of the tile within its request
+  int row0;           // first position of the tile within its request
   int kv_page_begin;  // absolute position of the request's first page in kv_indices
   int pad;
 };
@@ -43,9 +57,19 @@ struct alignas(32) PrefillTile {
 struct PrefillHeader {
   int num_tiles;
   int error;
+  int bm;
+  int pad;
 };
 
-size_t tile_capacity(int batch, int64_t total_q) { return size_t(total_q / kTileRows + batch + 1); }
+// Query positions per workgroup: about `rows` (position, head) rows, where
+// rows = 128 for head_dim <= 128 (two row blocks per wave) and 64 for 256.
+int rows_per_tile(int group, int head_dim) {
+  const int rows = head_dim <= 128 ? 128 : 64;
+  const int bm = (rows / group) / 16 * 16;
+  return bm < kMinRows ? kMinRows : bm;
+}
+
+size_t tile_capacity(int batch, int64_t total_q) { return size_t(total_q / kMinRows + batch + 1); }
 
 size_t prefill_ws_bytes(int batch, int64_t total_q) {
   return 256 + mi::align_up(tile_capacity(batch, total_q) * sizeof(PrefillTile), 256);
@@ -57,55 +81,73 @@ struct PlanParams {
   const int32_t* last_page_len;
   int batch;
   int capacity;
+  int bm;
   PrefillHeader* header;
   PrefillTile* tiles;
 };
 
-__global__ __launch_bounds__(1024) void prefill_plan_kernel(PlanParams p) {
-  __shared__ int buf[1024];
-  __shared__ int total_sh;
+// Inclusive scan over the block; *total gets the block-wide sum.  Ends with a
+// barrier so `buf` may be reused at once.
+__device__ int block_scan(int v, int* buf, int* total) {
   const int t = threadIdx.x;
-  int running = 0;
-  for (int base = 0; base < p.batch; base += blockDim.x) {
-    const int b = base + t;
-    int nt = 0, qo = 0, kv = 0, np = 0;
-    if (b < p.batch) {
-      qo = max(0, p.qo_indptr[b + 1] - p.qo_indptr[b]);
-      np = max(0, p.kv_indptr[b + 1] - p.kv_indptr[b]);
-      kv = np > 0 ? (np - 1) * kPageSize + min(max(p.last_page_len[b], 1), kPageSize) : 0;
-      nt = (qo + kTileRows - 1) / kTileRows;
-    }
-    buf[t] = nt;
+  buf[t] = v;
+  __syncthreads();
+  for (int o = 1; o < int(blockDim.x); o <<= 1) {
+    const int add = (t >= o) ? buf[t - o] : 0;
     __syncthreads();
-    for (int o = 1; o < int(blockDim.x); o <<= 1) {
-      const int add = (t >= o) ? buf[t - o] : 0;
-      __syncthreads();
-      buf[t] += add;
-      __syncthreads();
-    }
-    const int first = running + buf[t] - nt;
-    if (t == 0) total_sh = buf[blockDim.x - 1];
-    __syncthreads();
-    for (int k = 0; k < nt; ++k) {
-      const int idx = first + k;
-      if (idx >= p.capacity) break;
-      PrefillTile tile;
-      tile.b = b;
-      tile.row0 = (nt - 1 - k) * kTileRows;
-      tile.q_begin = p.qo_indptr[b] + tile.row0;
-      tile.q_rows = min(kTileRows, qo - tile.row0);
-      tile.qo_len = qo;
-      tile.kv_len = kv;
-      tile.kv_page_begin = p.kv_indptr[b];
-      tile.pad = 0;
-      p.tiles[idx] = tile;
-    }
-    running += total_sh;
+    buf[t] += add;
     __syncthreads();
   }
+  const int r = buf[t];
+  *total = buf[blockDim.x - 1];
+  __syncthreads();
+  return r;
+}
+
+// Tile order: requests by decreasing prompt length (ties by index), each
+// request's tiles from the end of its prompt (most keys) to the start.  The
+// run kernel maps consecutive tiles of one (request, KV head) to consecutive
+// workgroups of one XCD, so they share the request's K / V in that XCD's L2.
+__global__ __launch_bounds__(1024) void prefill_plan_kernel(PlanParams p) {
+  __shared__ int buf[1024];
+  const int t = threadIdx.x;
+  int total = 0;
+  for (int base = 0; base < p.batch; base += blockDim.x) {
+    const int b = base + t;
+    int nt = 0, start = 0;
+    if (b < p.batch) {
+      const int qo = max(0, p.qo_indptr[b + 1] - p.qo_indptr[b]);
+      nt = (qo + p.bm - 1) / p.bm;
+      // tiles of the requests ordered before b
+      for (int c = 0; c < p.batch; ++c) {
+        const int qc = max(0, p.qo_indptr[c + 1] - p.qo_indptr[c]);
+        if (qc > qo || (qc == qo && c < b)) start += (qc + p.bm - 1) / p.bm;
+      }
+      if (start + nt <= p.capacity) {
+        const int np = max(0, p.kv_indptr[b + 1] - p.kv_indptr[b]);
+        const int kv = np > 0 ? (np - 1) * kPageSize + min(max(p.last_page_len[b], 1), kPageSize) : 0;
+        for (int k = 0; k < nt; ++k) {
+          PrefillTile tile;
+          tile.b = b;
+          tile.row0 = (nt - 1 - k) * p.bm;
+          tile.q_begin = p.qo_indptr[b] + tile.row0;
+          tile.q_rows = min(p.bm, qo - tile.row0);
+          tile.qo_len = qo;
+          tile.kv_len = kv;
+          tile.kv_page_begin = p.kv_indptr[b];
+          tile.pad = 0;
+          p.tiles[start + k] = tile;
+        }
+      }
+    }
+    int chunk_total = 0;
+    block_scan(nt, buf, &chunk_total);
+    total += chunk_total;
+  }
   if (t == 0) {
-    p.header->num_tiles = min(running, p.capacity);
-    p.header->error = running > p.capacity ? 1 : 0;
+    p.header->num_tiles = min(total, p.capacity);
+    p.header->error = total > p.capacity ? 1 : 0;
+    p.header->bm = p.bm;
   }
 }
 
@@ -120,166 +162,301 @@ struct RunParams {
   uint16_t* out;
   int64_t o_st, o_sh;
   int64_t total_q;
-  int hkv, group, causal;
+  int hkv, group, causal, bm;
   float scale_log2;
 };
 
-template <int D>
-__global__ __launch_bounds__(256) void prefill_run_kernel(RunParams p) {
-  constexpr int KSTEPS = D / 32;
-  constexpr int NT = D / 16;
-  constexpr int VT_STRIDE = kKvTile + 8;  // bf16 per transposed row (80 bytes)
-  __shared__ __attribute__((aligned(16))) uint16_t vt[D * VT_STRIDE];
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
+typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+typedef __attribute__((ext_vector_type(8))) short s16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
+typedef __attribute__((ext_vector_type(8))) float f32x8_v;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_v;
+typedef __attribute__((address_space(3))) char lds_t;
 
-  const int hq = blockIdx.y;
-  const int hkv = hq / p.group;
+__device__ __forceinline__ void lds_store16(lds_t* p, u32x4_t v) { *(__attribute__((address_space(3))) u32x4_t*)p = v; }
+__device__ __forceinline__ u32x4_t lds_load16(const lds_t* p) {
+  return *(const __attribute__((address_space(3))) u32x4_t*)p;
+}
+// gfx950 LDS transpose read: the 16 lanes of a group address 4 rows x 16
+// bf16 (lane j: row j/4, elements 4*(j%4)..+3) and lane j receives column j.
+__device__ __forceinline__ s16x4_t lds_read_tr16(const lds_t* p) {
+  typedef __attribute__((address_space(3))) bf16x4_t lds_v4;
+  return __builtin_bit_cast(s16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4*)p));
+}
+__device__ __forceinline__ float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ int wave_max_i(int x) {
+  for (int o = 32; o > 0; o >>= 1) x = max(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int D, int MAXRB_>
+struct PrefillTraits {
+  static constexpr int KSTEPS = D / 32;            // 16x16x32 MFMAs per 16-key block of S^T
+  static constexpr int NT = D / 16;                // 16-wide head_dim tiles of O
+  static constexpr int CPR = D / 8;                // 16-byte chunks per token row
+  static constexpr int LOADS = kKvTile * CPR / 256;  // 16-byte loads per thread per tile, K and V each
+  static constexpr int RS = D * 2 + 16;            // LDS row stride (16 B pad spreads the banks)
+  static constexpr int TILE = kKvTile * RS;        // bytes of one staged K or V tile
+  static constexpr int MAXRB = MAXRB_;             // row blocks per wave
+};
+
+template <int D, int MAXRB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? PREFILL_WAVES : 1))) void prefill_run_kernel(RunParams p) {
+  using T = PrefillTraits<D, MAXRB>;
+  __shared__ __attribute__((aligned(16))) char smem[2 * 2 * T::TILE];  // [buffer][K, V]
+  lds_t* lds = (lds_t*)smem;
+
+  const int tile_idx = int(blockIdx.x) / p.hkv;
+  const int hkv = int(blockIdx.x) - tile_idx * p.hkv;
+  if (tile_idx >= p.header->num_tiles) return;  // whole workgroup
+  const PrefillTile t = p.tiles[tile_idx];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int n = lane & 15, kb = lane >> 4;
+  const int g = lane >> 4, n = lane & 15;
+  const int off = t.kv_len - t.qo_len;
+  const int pblocks = p.bm / 16;          // position blocks per head
+  const int nrb = pblocks * p.group;      // row blocks of the workgroup
+
   const int64_t tok_stride = int64_t(p.hkv) * D;
   const int64_t kv_stride = kPageSize * tok_stride;
   const int64_t page_stride = 2 * kv_stride;
-  const int num_tiles = p.header->num_tiles;
 
-  for (int ti = blockIdx.x; ti < num_tiles; ti += gridDim.x) {
-    const PrefillTile t = p.tiles[ti];
-    const int off = t.kv_len - t.qo_len;
-    const int local = 16 * w + n;  // this lane's query row within the tile
-    const bool qvalid = local < t.q_rows && (t.q_begin + local) < p.total_q;
-    mi::bf16x8_t qb[KSTEPS];
-    {
-      const uint16_t* qrow = p.q + int64_t(t.q_begin + (qvalid ? local : 0)) * p.q_st + int64_t(hq) * p.q_sh + kb * 8;
+  // ---- this wave's row blocks: rb = w, w + 4
+  mi::bf16x8_t qb[T::MAXRB][T::KSTEPS];
+  mi::f32x4_t o[T::MAXRB][T::NT];
+  float m_run[T::MAXRB], l_run[T::MAXRB];
+  int qpos[T::MAXRB];     // request-relative position of this lane's row n (-1: none)
+  int rb_hi[T::MAXRB];    // keys this row block needs (causal)
+  int head[T::MAXRB];
+  int nblk = 0;
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) {
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (qvalid) v = mi::load16(qrow + s * 32);
-        qb[s] = mi::as_bf16x8(v);
+  for (int r = 0; r < T::MAXRB; ++r) {
+    const int rb = w + 4 * r;
+    const bool has = rb < nrb;
+    nblk += has ? 1 : 0;
+    const int hg = has ? rb / pblocks : 0;
+    const int pb = has ? rb - hg * pblocks : 0;
+    head[r] = hkv * p.group + hg;
+    const int local = pb * 16 + n;
+    const bool valid = has && local < t.q_rows;
+    qpos[r] = valid ? t.row0 + local : -1;
+    const int last = t.row0 + min(pb * 16 + 15, t.q_rows - 1);
+    rb_hi[r] = !has ? 0 : (p.causal ? min(t.kv_len, last + off + 1) : t.kv_len);
+    const uint16_t* qrow = p.q + int64_t(t.q_begin + (valid ? local : 0)) * p.q_st + int64_t(head[r]) * p.q_sh + g * 8;
+#pragma unroll
+    for (int s = 0; s < T::KSTEPS; ++s) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (valid) v = mi::load16(qrow + s * 32);
+      qb[r][s] = mi::as_bf16x8(v);
+    }
+#pragma unroll
+    for (int j = 0; j < T::NT; ++j) o[r][j] = mi::f32x4_t{0.f, 0.f, 0.f, 0.f};
+    m_run[r] = -INFINITY;
+    l_run[r] = 0.f;
+  }
+  // smallest valid row position of the wave (for the unmasked-tile test)
+  int qmin = 0x7fffffff;
+#pragma unroll
+  for (int r = 0; r < T::MAXRB; ++r)
+    if (qpos[r] >= 0) qmin = min(qmin, qpos[r]);
+  qmin = -wave_max_i(-qmin);
+  int block_hi = p.causal ? min(t.kv_len, t.row0 + t.q_rows + off) : t.kv_len;
+  block_hi = max(block_hi, 0);
+  const int ntile = (block_hi + kKvTile - 1) / kKvTile;
+
+  // ---- staging.  Chunk c = thread + 256 i of a tile is token c / CPR, 16-byte
+  // chunk c % CPR.  Page ids are fetched one tile ahead of the K/V loads, so
+  // the loads never wait on an index load.
+  u32x4_t kreg[T::LOADS], vreg[T::LOADS];
+  int pid[T::LOADS];
+  auto fetch_ids = [&](int kt) {
+    const int kv0 = kt * kKvTile;
+#pragma unroll
+    for (int i = 0; i < T::LOADS; ++i) {
+      const int j = kv0 + (int(threadIdx.x) + 256 * i) / T::CPR;
+      pid[i] = (kt < ntile && j < t.kv_len) ? p.indices[t.kv_page_begin + j / kPageSize] : -1;
+    }
+  };
+  auto load_tile = [&](int kt) {
+    const int kv0 = kt * kKvTile;
+#pragma unroll
+    for (int i = 0; i < T::LOADS; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int tok = c / T::CPR, dc = c - tok * T::CPR;
+      const int j = kv0 + tok;
+      u32x4_t kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
+      const int64_t page = pid[i];
+      if (page >= 0 && page < p.num_pages) {
+        const uint16_t* src = p.pool + page * page_stride + (j % kPageSize) * tok_stride + int64_t(hkv) * D + dc * 8;
+        kv = __builtin_bit_cast(u32x4_t, mi::load16(src));
+        vv = __builtin_bit_cast(u32x4_t, mi::load16(src + kv_stride));
+      }
+      kreg[i] = kv;
+      vreg[i] = vv;
+    }
+  };
+  auto store_tile = [&](int buf) {
+    lds_t* kl = lds + buf * 2 * T::TILE;
+    lds_t* vl = kl + T::TILE;
+#pragma unroll
+    for (int i = 0; i < T::LOADS; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int tok = c / T::CPR, dc = c - tok * T::CPR;
+      lds_store16(kl + tok * T::RS + dc * 16, kreg[i]);
+      lds_store16(vl + tok * T::RS + dc * 16, vreg[i]);
+    }
+  };
+
+  if (ntile > 0) {
+    fetch_ids(0);
+    load_tile(0);
+    fetch_ids(1);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int kt = 0; kt < ntile; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < ntile) {
+      load_tile(kt + 1);
+      fetch_ids(kt + 2);
+    }
+    const int kv0 = kt * kKvTile;
+    const lds_t* kl = lds + buf * 2 * T::TILE;
+    const lds_t* vl = kl + T::TILE;
+    // All of the wave's row blocks are computed together so each K / V
+    // operand read from LDS feeds MAXRB MFMAs.  A block with nothing left to
+    // do (causally finished, or absent: qpos = -1) masks every key and adds
+    // exactly zero, so no per-block branches are needed.
+    bool any = false;
+#pragma unroll
+    for (int r = 0; r < T::MAXRB; ++r) any = any || (r < nblk && kv0 < rb_hi[r]);
+    if (any) {
+      // No key of the tile needs a mask: all are < kv_len and (causal) visible
+      // to the wave's first valid row.  (Rows past the tile's end hold zero
+      // queries and are never written, so they need no mask either.)
+      const bool full = kv0 + kKvTile <= t.kv_len && (!p.causal || kv0 + kKvTile - 1 <= qmin + off);
+      // ---- S^T for the tile's four 16-key blocks (raw scores; the softmax
+      // scale is applied inside the exponent)
+      float sv[T::MAXRB][4][4];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        mi::bf16x8_t ka[T::KSTEPS];
+#pragma unroll
+        for (int s = 0; s < T::KSTEPS; ++s)
+          ka[s] = __builtin_bit_cast(mi::bf16x8_t, lds_load16(kl + (kb * 16 + n) * T::RS + (4 * s + g) * 16));
+#pragma unroll
+        for (int r = 0; r < T::MAXRB; ++r) {
+          mi::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s = 0; s < T::KSTEPS; ++s) c = mi::mfma_16x16x32_bf16(ka[s], qb[r][s], c);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sv[r][kb][i] = c[i];
+          if (!full) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int j = kv0 + kb * 16 + 4 * g + i;
+              const bool ok = qpos[r] >= 0 && j < t.kv_len && (!p.causal || j <= qpos[r] + off);
+              if (!ok) sv[r][kb][i] = -INFINITY;
+            }
+          }
+        }
+      }
+      // ---- online softmax per row, lazy rescale; P packed as the A operand
+      mi::bf16x8_t pa[T::MAXRB][2];
+#pragma unroll
+      for (int r = 0; r < T::MAXRB; ++r) {
+        float mloc = sv[r][0][0];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mloc = fmaxf(mloc, sv[r][kb][i]);
+        mloc = max_xor32(max_xor16(mloc)) * p.scale_log2;  // scale > 0 keeps the arg max
+        const bool need = mloc > m_run[r] + kLazyRescale;
+        if (__builtin_amdgcn_ballot_w64(need)) {
+          const float mnew = need ? mloc : m_run[r];
+          const float f = need ? ((m_run[r] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[r] - mnew)) : 1.f;
+          m_run[r] = mnew;
+          l_run[r] *= f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float fo = mi::lane_shuffle(f, 4 * g + i);
+#pragma unroll
+            for (int j = 0; j < T::NT; ++j) o[r][j][i] *= fo;
+          }
+        }
+        // exp2(-inf - m) = 0 for masked keys; m is taken as 0 while the row
+        // has seen no key (m_run still -inf), avoiding -inf - -inf
+        const float m_use = (m_run[r] == -INFINITY) ? 0.f : m_run[r];
+        float pv[4][4];
+        float ps = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            pv[kb][i] = __builtin_amdgcn_exp2f(fmaf(sv[r][kb][i], p.scale_log2, -m_use));
+            ps += pv[kb][i];
+          }
+        l_run[r] += ps;
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr)
+          pa[r][pr] = __builtin_bit_cast(
+              mi::bf16x8_t,
+              __builtin_convertvector((f32x8_v){pv[2 * pr][0], pv[2 * pr][1], pv[2 * pr][2], pv[2 * pr][3],
+                                                pv[2 * pr + 1][0], pv[2 * pr + 1][1], pv[2 * pr + 1][2],
+                                                pv[2 * pr + 1][3]},
+                                      bf16x8_v));
+      }
+      // ---- O += P V over key blocks (0, 1) and (2, 3)
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr) {
+        const lds_t* v0 = vl + (2 * pr * 16 + 4 * g + (n >> 2)) * T::RS + (n & 3) * 8;
+        const lds_t* v1 = v0 + 16 * T::RS;
+#pragma unroll
+        for (int j = 0; j < T::NT; ++j) {
+          const s16x4_t a = lds_read_tr16(v0 + 32 * j), b = lds_read_tr16(v1 + 32 * j);
+          const mi::bf16x8_t vb =
+              __builtin_bit_cast(mi::bf16x8_t, (s16x8_t){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]});
+#pragma unroll
+          for (int r = 0; r < T::MAXRB; ++r) o[r][j] = mi::mfma_16x16x32_bf16(pa[r][pr], vb, o[r][j]);
+        }
       }
     }
-    int wave_hi = 0;
-    if (16 * w < t.q_rows) {
-      const int last_row = t.row0 + min(16 * w + 15, t.q_rows - 1);
-      wave_hi = p.causal ? min(t.kv_len, last_row + off + 1) : t.kv_len;
-    }
-    int block_hi = p.causal ? min(t.kv_len, t.row0 + t.q_rows + off) : t.kv_len;
-    block_hi = max(block_hi, 0);
-    const int ntile = (block_hi + kKvTile - 1) / kKvTile;
+    if (kt + 1 < ntile) store_tile(buf ^ 1);
+    __syncthreads();
+  }
 
-    mi::f32x4_t o[NT];
+  // ---- normalise and store: lane (g, n) holds rows 4g + i, column 16j + n
 #pragma unroll
-    for (int j = 0; j < NT; ++j) o[j] = mi::f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.f;
-    const int qr = t.row0 + local;  // request-relative query index
-
-    for (int kt = 0; kt < ntile; ++kt) {
-      const int kv0 = kt * kKvTile;
-      __syncthreads();
-      for (int c = threadIdx.x; c < kKvTile * (D / 8); c += blockDim.x) {
-        const int kv = c / (D / 8), dc = c - kv * (D / 8);
-        const int j = kv0 + kv;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        const int64_t page = j < t.kv_len ? p.indices[t.kv_page_begin + j / kPageSize] : -1;
-        if (page >= 0 && page < p.num_pages) {
-          v = mi::load16(p.pool + page * page_stride + kv_stride + (j % kPageSize) * tok_stride +
-                         int64_t(hkv) * D + dc * 8);
-        }
-        uint16_t* col = vt + (dc * 8) * VT_STRIDE + kv;
-        col[0 * VT_STRIDE] = uint16_t(v.x);
-        col[1 * VT_STRIDE] = uint16_t(v.x >> 16);
-        col[2 * VT_STRIDE] = uint16_t(v.y);
-        col[3 * VT_STRIDE] = uint16_t(v.y >> 16);
-        col[4 * VT_STRIDE] = uint16_t(v.z);
-        col[5 * VT_STRIDE] = uint16_t(v.z >> 16);
-        col[6 * VT_STRIDE] = uint16_t(v.w);
-        col[7 * VT_STRIDE] = uint16_t(v.w >> 16);
-      }
-      __syncthreads();
-      if (kv0 >= wave_hi) continue;
-
-      // ---- S^T = K Q^T for keys kv0 + g*16 + (0..15)
-      float sv[2][4];
-#pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        const int jk = kv0 + g * 16 + n;
-        uint4 ka[KSTEPS];
-        const int64_t kpage = jk < t.kv_len ? p.indices[t.kv_page_begin + jk / kPageSize] : -1;
-        if (kpage >= 0 && kpage < p.num_pages) {
-          const int64_t page = kpage;
-          const uint16_t* krow = p.pool + page * page_stride + (jk % kPageSize) * tok_stride + int64_t(hkv) * D + kb * 8;
-#pragma unroll
-          for (int s = 0; s < KSTEPS; ++s) ka[s] = mi::load16(krow + s * 32);
-        } else {
-#pragma unroll
-          for (int s = 0; s < KSTEPS; ++s) ka[s] = make_uint4(0, 0, 0, 0);
-        }
-        mi::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) c = mi::mfma_16x16x32_bf16(mi::as_bf16x8(ka[s]), qb[s], c);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int j = kv0 + g * 16 + 4 * kb + i;
-          const bool ok = qvalid && j < t.kv_len && (!p.causal || j <= qr + off);
-          sv[g][i] = ok ? c[i] * p.scale_log2 : -INFINITY;
-        }
-      }
-      // ---- online softmax for query row n (lanes n, n+16, n+32, n+48)
-      float mx = sv[0][0];
-#pragma unroll
-      for (int g = 0; g < 2; ++g)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sv[g][i]);
-      mx = fmaxf(mx, mi::lane_shuffle(mx, lane ^ 16));
-      mx = fmaxf(mx, mi::lane_shuffle(mx, lane ^ 32));
-      const float m_new = fmaxf(m_run, mx);
-      const bool dead = (m_new == -INFINITY);
-      const float alpha = dead ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
-      float pv[2][4];
-      float psum = 0.f;
-#pragma unroll
-      for (int g = 0; g < 2; ++g)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          pv[g][i] = dead ? 0.f : __builtin_amdgcn_exp2f(sv[g][i] - m_new);
-          psum += pv[g][i];
-        }
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
-      float ao[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ao[i] = mi::lane_shuffle(alpha, 4 * kb + i);
-#pragma unroll
-      for (int j = 0; j < NT; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[j][i] *= ao[i];
-
-      // ---- O += P V
-      uint4 pa_u;
-      pa_u.x = mi::pack_bf16x2(pv[0][0], pv[0][1]);
-      pa_u.y = mi::pack_bf16x2(pv[0][2], pv[0][3]);
-      pa_u.z = mi::pack_bf16x2(pv[1][0], pv[1][1]);
-      pa_u.w = mi::pack_bf16x2(pv[1][2], pv[1][3]);
-      const mi::bf16x8_t pa = mi::as_bf16x8(pa_u);
-#pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        const uint16_t* row = vt + (j * 16 + n) * VT_STRIDE;
-        const uint2 lo = *reinterpret_cast<const uint2*>(row + 4 * kb);
-        const uint2 hi = *reinterpret_cast<const uint2*>(row + 16 + 4 * kb);
-        const uint4 vb = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        o[j] = mi::mfma_16x16x32_bf16(pa, mi::as_bf16x8(vb), o[j]);
-      }
-    }
-
-    // ---- normalise and store: lane holds rows 4*kb + i, column j*16 + n
-    float l_tot = l_run + mi::lane_shuffle(l_run, lane ^ 16);
-    l_tot += mi::lane_shuffle(l_tot, lane ^ 32);
+  for (int r = 0; r < T::MAXRB; ++r) {
+    if (r >= nblk) continue;
+    const float lt = sum_xor32(sum_xor16(l_run[r]));
+    const int rb = w + 4 * r;
+    const int pb = rb - (rb / pblocks) * pblocks;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float li = mi::lane_shuffle(l_tot, 4 * kb + i);
+      const float li = mi::lane_shuffle(lt, 4 * g + i);
       const float inv = li > 0.f ? 1.f / li : 0.f;
-      const int r = 16 * w + 4 * kb + i;
-      if (r < t.q_rows && t.q_begin + r < p.total_q) {
-        uint16_t* orow = p.out + int64_t(t.q_begin + r) * p.o_st + int64_t(hq) * p.o_sh;
+      const int local = pb * 16 + 4 * g + i;
+      if (local < t.q_rows && t.q_begin + local < p.total_q) {
+        uint16_t* orow = p.out + int64_t(t.q_begin + local) * p.o_st + int64_t(head[r]) * p.o_sh;
 #pragma unroll
-        for (int j = 0; j < NT; ++j) orow[j * 16 + n] = mi::f32_to_bf16(o[j][i] * inv);
+        for (int j = 0; j < T::NT; ++j) orow[j * 16 + n] = mi::f32_to_bf16(o[r][j][i] * inv);
       }
     }
   }
@@ -294,10 +471,15 @@ extern "C" size_t mi_prefill_workspace_size(int32_t batch_size, int64_t total_q)
 
 extern "C" int mi_prefill_plan(void* workspace, size_t workspace_bytes, const int32_t* qo_indptr,
                                const int32_t* kv_indptr, const int32_t* kv_last_page_len,
-                               int32_t batch_size, int64_t total_q, int32_t page_size,
+                               int32_t batch_size, int64_t total_q, int32_t num_qo_heads,
+                               int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                                mi_stream_t stream) {
   mi::clear_error();
   if (batch_size < 0 || total_q < 0) return mi::fail(MI_ERR_INVALID, "prefill plan: negative sizes");
+  if (num_qo_heads <= 0 || num_kv_heads <= 0 || num_qo_heads % num_kv_heads)
+    return mi::fail(MI_ERR_INVALID, "prefill plan: bad head counts (%d, %d)", num_qo_heads, num_kv_heads);
+  if (num_qo_heads / num_kv_heads > 8)
+    return mi::fail(MI_ERR_UNSUPPORTED, "prefill plan: group %d (built for 1..8)", num_qo_heads / num_kv_heads);
   if (page_size != kPageSize) return mi::fail(MI_ERR_UNSUPPORTED, "prefill plan: page_size %d (built for 16)", page_size);
   const size_t need = prefill_ws_bytes(batch_size, total_q);
   if (!workspace || workspace_bytes < need)
@@ -311,6 +493,7 @@ extern "C" int mi_prefill_plan(void* workspace, size_t workspace_bytes, const in
   pp.last_page_len = kv_last_page_len;
   pp.batch = batch_size;
   pp.capacity = int(tile_capacity(batch_size, total_q));
+  pp.bm = rows_per_tile(num_qo_heads / num_kv_heads, head_dim);
   pp.header = reinterpret_cast<PrefillHeader*>(ws);
   pp.tiles = reinterpret_cast<PrefillTile*>(ws + 256);
   hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream), pp);
@@ -327,10 +510,11 @@ extern "C" int mi_prefill_run(void* workspace, size_t workspace_bytes, const voi
   mi::clear_error();
   if (batch_size < 0 || total_q < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || num_qo_heads % num_kv_heads)
     return mi::fail(MI_ERR_INVALID, "prefill run: bad sizes");
+  if (num_qo_heads / num_kv_heads > 8)
+    return mi::fail(MI_ERR_UNSUPPORTED, "prefill run: group %d (built for 1..8)", num_qo_heads / num_kv_heads);
   if (page_size != kPageSize) return mi::fail(MI_ERR_UNSUPPORTED, "prefill run: page_size %d (built for 16)", page_size);
-  if (head_dim != 64 && head_dim != 128)
-    return mi::fail(MI_ERR_UNSUPPORTED, "prefill run: head_dim %d (built for 64, 128)", head_dim);
-  if (num_qo_heads > 65535) return mi::fail(MI_ERR_INVALID, "prefill run: too many heads");
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return mi::fail(MI_ERR_UNSUPPORTED, "prefill run: head_dim %d (built for 64, 128, 256)", head_dim);
   const size_t need = prefill_ws_bytes(batch_size, total_q);
   if (!workspace || workspace_bytes < need)
     return mi::fail(MI_ERR_WORKSPACE, "prefill run: workspace %zu bytes, need %zu", workspace_bytes, need);
@@ -339,6 +523,8 @@ extern "C" int mi_prefill_run(void* workspace, size_t workspace_bytes, const voi
   if ((reinterpret_cast<uintptr_t>(q) & 15) || (reinterpret_cast<uintptr_t>(paged_kv_cache) & 15) ||
       q_stride_token % 8 || q_stride_head % 8)
     return mi::fail(MI_ERR_INVALID, "prefill run: q rows and pool must be 16-byte aligned");
+  const int64_t grid = int64_t(tile_capacity(batch_size, total_q)) * num_kv_heads;
+  if (grid > 0x7fffffff) return mi::fail(MI_ERR_INVALID, "prefill run: too many tiles");
   char* ws = static_cast<char*>(workspace);
   RunParams rp;
   rp.header = reinterpret_cast<const PrefillHeader*>(ws);
@@ -356,14 +542,15 @@ extern "C" int mi_prefill_run(void* workspace, size_t workspace_bytes, const voi
   rp.hkv = num_kv_heads;
   rp.group = num_qo_heads / num_kv_heads;
   rp.causal = causal ? 1 : 0;
+  rp.bm = rows_per_tile(rp.group, head_dim);
   const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf(float(head_dim));
   rp.scale_log2 = scale * mi::kLog2e;
-  int64_t gx = int64_t(tile_capacity(batch_size, total_q));
-  if (gx > 65535) gx = 65535;
-  const dim3 grid{static_cast<uint32_t>(gx), static_cast<uint32_t>(num_qo_heads), 1u};
-  if (head_dim == 64)
-    hipLaunchKernelGGL(prefill_run_kernel<64>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), rp);
-  else
-    hipLaunchKernelGGL(prefill_run_kernel<128>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), rp);
+  const dim3 g{static_cast<uint32_t>(grid), 1u, 1u};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (head_dim) {
+    case 64: hipLaunchKernelGGL((prefill_run_kernel<64, 2>), g, dim3(256), 0, s, rp); break;
+    case 128: hipLaunchKernelGGL((prefill_run_kernel<128, 2>), g, dim3(256), 0, s, rp); break;
+    default: hipLaunchKernelGGL((prefill_run_kernel<256, 1>), g, dim3(256), 0, s, rp); break;
+  }
   return mi::check_launch("prefill_run_kernel");
 }

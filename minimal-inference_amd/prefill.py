@@ -79,7 +79,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
             max_total_q = self._capacity_rows(batch)
         _lib.call("mi_prefill_plan", self._ws.data_ptr(), self._ws_bytes, qo_indptr.data_ptr(),
                   paged_kv_indptr.data_ptr(), paged_kv_last_page_len.data_ptr(), batch, max_total_q,
-                  page_size, stream_of(qo_indptr))
+                  num_qo_heads, num_kv_heads, head_dim_qk, page_size, stream_of(qo_indptr))
         self._batch, self._max_total_q = batch, max_total_q
         self._hq, self._hkv, self._d, self._ps = num_qo_heads, num_kv_heads, head_dim_qk, page_size
         self._indices = paged_kv_indices
