@@ -252,7 +252,7 @@ struct DecodeTraits {
   static constexpr int CPR = D / 8;      // 16-byte chunks per token row of one head
   static constexpr int LPI = CPR / 4;    // 16-byte loads per lane per page, for K and for V
   static constexpr int RS = D * 2 + 16;  // LDS row stride in bytes (16 B pad spreads the banks)
-  static constexpr int SLOT = 2 * kPageSize * RS;  // one page of K and V in LDS
+  static constexpr int SLOT = 4 * kPageSize * RS;  // two pages of K and V in LDS
   // Pages in flight per wave (~128-160 registers of staging).
   static constexpr int NB = (D == 64) ? MI_DECODE_NB64 : (D == 128) ? MI_DECODE_NB128 : 2;
   static constexpr int OUT = D / 64;  // merged outputs per head per lane
@@ -261,6 +261,7 @@ struct DecodeTraits {
   static constexpr int KB = KB_RAW > 16 ? 16 : (KB_RAW < 1 ? 1 : KB_RAW);
   static_assert(G >= 1 && G <= 16, "group size");
   static_assert((NB - 1) * 2 * LPI <= 63, "vmcnt range");
+  static_assert(NB % 2 == 0, "pages are consumed in pairs");
 };
 
 struct RunParams {
@@ -317,6 +318,9 @@ __device__ __forceinline__ s16x4_t lds_read_tr16(const lds_t* p) {
 
 typedef __attribute__((ext_vector_type(4))) float f32x4_v;
 typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4_v;
+typedef __attribute__((ext_vector_type(8))) float f32x8_v;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_v;
+typedef __attribute__((ext_vector_type(8))) short s16x8_t;
 
 // Max / sum of x and its value in lane ^ 16 (resp. lane ^ 32), with the
 // gfx950 lane-swap instructions: swapping x with itself leaves x in one
@@ -428,12 +432,19 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
   float m_run = -INFINITY;  // head j
   float l_run = 0.f;        // head j, this lane's tokens
 
-  lds_t* kl = lds;
-  lds_t* vl = lds + kPageSize * T::RS;
+  // LDS slots: page a of a pair at [0, 2 pages), page b after it
+  auto k_slot = [&](int which) { return lds + which * 2 * kPageSize * T::RS; };
+  auto v_slot = [&](int which) { return lds + which * 2 * kPageSize * T::RS + kPageSize * T::RS; };
 
-  auto consume = [&](const Regs& r, int valid) {
-    // ---- the page to LDS (V rows past `valid` as zeros on a partial page:
-    // P is 0 there, but 0 * NaN would poison the MFMA)
+  // Two pages (32 tokens) per step: one softmax update, and O += P V as
+  // 16x16x32 MFMAs whose A operand is the pair of S^T accumulators (lane
+  // (g, j) holds tokens 4g+i of both pages) and whose B operand is the two
+  // pages' transpose reads in the same token order.
+  auto stage = [&](const Regs& r, int valid, int which) {
+    // the page to LDS (V rows past `valid` as zeros on a partial page: P is
+    // 0 there, but 0 * NaN would poison the MFMA)
+    lds_t* kl = k_slot(which);
+    lds_t* vl = v_slot(which);
 #pragma unroll
     for (int i = 0; i < T::LPI; ++i)
       lds_store16(kl + (lrow + 8 * (i & 1)) * T::RS + (lchunk + 8 * (i >> 1)) * 16, r.k[i]);
@@ -448,17 +459,25 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
         lds_store16(vl + row * T::RS + (lchunk + 8 * (i >> 1)) * 16, (row < valid) ? r.v[i] : u32x4_t{0, 0, 0, 0});
       }
     }
-    // ---- S^T = K Q^T
+  };
+  auto scores = [&](int which, int valid, float (&sv)[4]) {
+    const lds_t* kl = k_slot(which);
     mi::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < T::KSTEPS; ++s)
       c = mi::mfma_16x16x32_bf16(__builtin_bit_cast(mi::bf16x8_t, lds_load16(kl + j * T::RS + (g + 4 * s) * 16)),
                                  qb[s], c);
-    float sv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) sv[i] = (4 * g + i < valid) ? c[i] * p.scale_log2 : -INFINITY;
+  };
+  auto consume2 = [&](const Regs& ra, int va, const Regs& rb, int vb) {
+    stage(ra, va, 0);
+    stage(rb, vb, 1);
+    float sa[4], sb[4];
+    scores(0, va, sa);
+    scores(1, vb, sb);
     // ---- online softmax for head j, lazy rescale
-    float mloc = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    float mloc = fmaxf(fmaxf(fmaxf(sa[0], sa[1]), fmaxf(sa[2], sa[3])), fmaxf(fmaxf(sb[0], sb[1]), fmaxf(sb[2], sb[3])));
     mloc = max_xor16(mloc);
     mloc = max_xor32(mloc);
     const bool need = mloc > m_run + kLazyRescale;
@@ -477,17 +496,25 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
     // exp2(-inf - m) = 0 for masked tokens; m is taken as 0 while no token
     // of the head has been seen (m_run still -inf), avoiding -inf - -inf
     const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
-    float pv[4];
+    float pv[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pv[i] = __builtin_amdgcn_exp2f(sv[i] - m_use);
-    l_run += (pv[0] + pv[1]) + (pv[2] + pv[3]);
-    const s16x4_t pa = __builtin_bit_cast(
-        s16x4_t, __builtin_convertvector((f32x4_v){pv[0], pv[1], pv[2], pv[3]}, bf16x4_v));
+    for (int i = 0; i < 4; ++i) {
+      pv[i] = __builtin_amdgcn_exp2f(sa[i] - m_use);
+      pv[4 + i] = __builtin_amdgcn_exp2f(sb[i] - m_use);
+    }
+    l_run += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+    const mi::bf16x8_t pa = __builtin_bit_cast(
+        mi::bf16x8_t,
+        __builtin_convertvector((f32x8_v){pv[0], pv[1], pv[2], pv[3], pv[4], pv[5], pv[6], pv[7]}, bf16x8_v));
     // ---- O += P V
-    const lds_t* vrow = vl + (4 * g + (j >> 2)) * T::RS + (j & 3) * 8;
+    const lds_t* va_row = v_slot(0) + (4 * g + (j >> 2)) * T::RS + (j & 3) * 8;
+    const lds_t* vb_row = v_slot(1) + (4 * g + (j >> 2)) * T::RS + (j & 3) * 8;
 #pragma unroll
-    for (int t = 0; t < T::NT; ++t)
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, lds_read_tr16(vrow + 32 * t), acc[t], 0, 0, 0);
+    for (int t = 0; t < T::NT; ++t) {
+      const s16x4_t x = lds_read_tr16(va_row + 32 * t), y = lds_read_tr16(vb_row + 32 * t);
+      const mi::bf16x8_t vbop = __builtin_bit_cast(mi::bf16x8_t, (s16x8_t){x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]});
+      acc[t] = mi::mfma_16x16x32_bf16(pa, vbop, acc[t]);
+    }
   };
 
   // ---- stream the pages: groups of page ids (the item's inline copy first,
@@ -508,16 +535,20 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
     const int full = gsize / T::NB;
     for (int it = 0; it < full; ++it) {
 #pragma unroll
-      for (int s = 0; s < T::NB; ++s) {
+      for (int s = 0; s < T::NB; s += 2) {
         const int k = it * T::NB + s;
-        consume(buf[s], page_valid(k));
+        consume2(buf[s], page_valid(k), buf[s + 1], page_valid(k + 1));
         issue(buf[s], k + T::NB, gsize);
+        issue(buf[s + 1], k + 1 + T::NB, gsize);
       }
     }
+    // the last rem (< NB) pages; a pair's second page past the group's end
+    // was loaded through a size-0 descriptor (zeros) and is fully masked
     const int rem = gsize - full * T::NB;
 #pragma unroll
-    for (int s = 0; s < T::NB - 1; ++s)
-      if (s < rem) consume(buf[s], page_valid(full * T::NB + s));
+    for (int s = 0; s < T::NB - 1; s += 2)
+      if (s < rem) consume2(buf[s], page_valid(full * T::NB + s), buf[s + 1],
+                            s + 1 < rem ? page_valid(full * T::NB + s + 1) : 0);
     g_start += gsize;
     if (g_start >= npg) break;
     gsize = min(64, npg - g_start);
