@@ -298,6 +298,19 @@ template <typename F>
 __device__ __forceinline__ void coherent_store(F* p, F v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Split partials: device-coherent (bypassing the XCD's L2) in general, or
+// L2-coherent only when every unit of a (request, KV head) runs on one XCD
+// (XL), which keeps the publish / merge round trips inside that L2.
+template <bool XL, typename F>
+__device__ __forceinline__ F partial_load(const F* p) {
+  if constexpr (XL) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  else return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool XL, typename F>
+__device__ __forceinline__ void partial_store(F* p, F v) {
+  if constexpr (XL) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  else __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
@@ -369,7 +382,7 @@ __device__ __forceinline__ int load_item_word(const RunParams& p, int u) {
 //                accumulator each lane already holds, and V comes from the
 //                LDS transpose read (lane (g, j) gets V[4g..4g+3][16t + j]);
 //                O[head 4g+i][16t + j] accumulates in registers.
-template <int D, int G>
+template <int D, int G, bool XL>
 __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, lds_t* lds) {
   using T = DecodeTraits<D, G>;
   using Regs = PageRegs<D, G>;
@@ -587,12 +600,12 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
       const int h = 4 * g + i;
       if (h < G) {
 #pragma unroll
-        for (int t = 0; t < T::NT; ++t) coherent_store(po + h * D + 16 * t + j, acc[t][i]);
+        for (int t = 0; t < T::NT; ++t) partial_store<XL>(po + h * D + 16 * t + j, acc[t][i]);
       }
     }
     if (lane < G) {  // lane h holds m_run / lt of head h
-      coherent_store(p.pml + (int64_t(u) * G + lane) * 2 + 0, m_run);
-      coherent_store(p.pml + (int64_t(u) * G + lane) * 2 + 1, lt);
+      partial_store<XL>(p.pml + (int64_t(u) * G + lane) * 2 + 0, m_run);
+      partial_store<XL>(p.pml + (int64_t(u) * G + lane) * 2 + 1, lt);
     }
   }
   // Wait until this wave's write-through stores are acknowledged (vmcnt 0;
@@ -626,7 +639,7 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
 #pragma unroll
       for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int k = 0; k < T::OUT; ++k) v[q][h][k] = coherent_load(src + h * D + lane + 64 * k);
+        for (int k = 0; k < T::OUT; ++k) v[q][h][k] = partial_load<XL>(src + h * D + lane + 64 * k);
     }
   };
   for (int r0 = 0; r0 < nsplit; r0 += 64) {
@@ -635,8 +648,8 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
     float ms[G], ls[G], wgt[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      ms[h] = coherent_load(p.pml + (int64_t(my_unit) * G + h) * 2 + 0);
-      ls[h] = coherent_load(p.pml + (int64_t(my_unit) * G + h) * 2 + 1);
+      ms[h] = partial_load<XL>(p.pml + (int64_t(my_unit) * G + h) * 2 + 0);
+      ls[h] = partial_load<XL>(p.pml + (int64_t(my_unit) * G + h) * 2 + 1);
     }
     float v[T::KB][G][T::OUT];
     load_rows(v, r0, 0, nr);
@@ -678,7 +691,7 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
 
 // head_dim <= 128: registers capped at 256 per wave, so at least two waves
 // share a SIMD (8 units per CU).  head_dim 256 needs the full register file.
-template <int D, int G>
+template <int D, int G, bool XL>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(D <= 128 ? MI_DECODE_WAVES : 1))) void decode_run_kernel(
     RunParams p) {
   __shared__ __attribute__((aligned(16))) char slot[DecodeTraits<D, G>::SLOT];
@@ -689,7 +702,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(D <= 128 ? M
   int iv = load_item_word(p, u);
   const int num_units = p.header->num_units;
   while (u < num_units) {
-    decode_unit<D, G>(p, u, iv, lds);
+    decode_unit<D, G, XL>(p, u, iv, lds);
     u += gridDim.x;
     if (u < num_units) iv = load_item_word(p, u);
   }
@@ -697,26 +710,26 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(D <= 128 ? M
 
 typedef void (*RunKernel)(RunParams);
 
-template <int D>
+template <int D, bool XL>
 RunKernel pick_group(int g) {
   switch (g) {
-    case 1: return decode_run_kernel<D, 1>;
-    case 2: return decode_run_kernel<D, 2>;
-    case 3: return decode_run_kernel<D, 3>;
-    case 4: return decode_run_kernel<D, 4>;
-    case 5: return decode_run_kernel<D, 5>;
-    case 6: return decode_run_kernel<D, 6>;
-    case 7: return decode_run_kernel<D, 7>;
-    case 8: return decode_run_kernel<D, 8>;
+    case 1: return decode_run_kernel<D, 1, XL>;
+    case 2: return decode_run_kernel<D, 2, XL>;
+    case 3: return decode_run_kernel<D, 3, XL>;
+    case 4: return decode_run_kernel<D, 4, XL>;
+    case 5: return decode_run_kernel<D, 5, XL>;
+    case 6: return decode_run_kernel<D, 6, XL>;
+    case 7: return decode_run_kernel<D, 7, XL>;
+    case 8: return decode_run_kernel<D, 8, XL>;
     default: return nullptr;
   }
 }
 
-RunKernel pick_kernel(int head_dim, int group) {
+RunKernel pick_kernel(int head_dim, int group, bool xl = false) {
   switch (head_dim) {
-    case 64: return pick_group<64>(group);
-    case 128: return pick_group<128>(group);
-    case 256: return pick_group<256>(group);
+    case 64: return xl ? pick_group<64, true>(group) : pick_group<64, false>(group);
+    case 128: return xl ? pick_group<128, true>(group) : pick_group<128, false>(group);
+    case 256: return xl ? pick_group<256, true>(group) : pick_group<256, false>(group);
     default: return nullptr;
   }
 }
@@ -750,6 +763,8 @@ extern "C" int mi_decode_plan(void* workspace, size_t workspace_bytes, const int
   mi::clear_error();
   int rc = check_shape("decode plan", batch_size, num_qo_heads, num_kv_heads, head_dim, page_size);
   if (rc) return rc;
+  // learn the workgroup -> XCD mapping once per device (outside captures)
+  (void)mi::xcd_round_robin(static_cast<hipStream_t>(stream), true);
   if (max_units <= 0) max_units = units_that_fit(workspace_bytes, batch_size, num_qo_heads, num_kv_heads, head_dim);
   const DecodeLayout L = decode_layout(batch_size, num_qo_heads, num_kv_heads, head_dim, max_units);
   if (!workspace || workspace_bytes < L.total)
@@ -814,8 +829,14 @@ extern "C" int mi_decode_run(void* workspace, size_t workspace_bytes, const void
   rp.max_items = L.max_items;
   const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf(float(head_dim));
   rp.scale_log2 = scale * mi::kLog2e;
-  RunKernel k = pick_kernel(head_dim, num_qo_heads / num_kv_heads);
   const int grid = min(max_units, mi::num_cus() * kUnitsPerCU);
+  // Units u = item * kv_heads + h run on workgroup u mod grid.  When
+  // workgroups go to XCDs round robin over n XCDs and n divides both
+  // kv_heads and the grid, every unit of one (request, KV head) lands on XCD
+  // h mod n, so the split partials can stay in that XCD's L2.
+  const int nx = mi::xcd_round_robin(static_cast<hipStream_t>(stream), false);
+  const bool xl = nx > 0 && num_kv_heads % nx == 0 && grid % nx == 0;
+  RunKernel k = pick_kernel(head_dim, num_qo_heads / num_kv_heads, xl);
   hipLaunchKernelGGL(k, dim3(grid), dim3(64), 0, static_cast<hipStream_t>(stream), rp);
   return mi::check_launch("decode_run_kernel");
 }
