@@ -8,8 +8,11 @@ and prefilled (one ragged batch) before timing.
 
 A "step" is one full decode step of the 32-request batch: device page-table
 step, plan(), graph replay (32 layers: GEMMs, RoPE, KV append, split-K paged
-attention, sampler) and the read-back of the sampled ids.  ``value`` is
-decoded tokens per second over exactly ``--steps`` timed steps.
+attention, sampler), the feedback of the sampled ids and, once per window of
+``--decode-window`` steps, end-of-sequence detection on the GPU and the
+read-back of the window's ids.  ``value`` is decoded tokens per second over
+exactly ``--steps`` timed steps; ``decode_tok_s_one_step_per_round_trip`` is
+the same over the next ``--steps`` steps with a read-back after every step.
 
 ``roofline`` is measured on the decode-attention kernel alone: after the
 timed steps, the 32 layers' attention launches (the batch's real page tables
@@ -33,8 +36,8 @@ the same batch.
 as repeated launches captured in one hipGraph and replayed between HIP events: the ragged
 causal prefill attention of the 32 prompts for one layer (MFMA bound:
 flops = sum_b 4 * H_q * D * L_b (L_b + 1) / 2, against 2.5 PFLOP/s bf16), the
-decode-step fused RoPE + KV append and the sampler for the 32 rows
-(latency bound: microseconds), and the device page-table step.
+decode-step fused RoPE + KV append (into a copy of layer 0's pool) and the
+sampler for the 32 rows (latency bound: microseconds).
 """
 
 from __future__ import annotations
@@ -118,8 +121,9 @@ def path_kernel_times(sch, cfg, reqs, lens, dev) -> dict:
     # decode-step fused RoPE + append for the batch's rows (writes the next position's slot)
     qkv = torch.randn(B, (hq + 2 * hkv) * d, device=dev, dtype=torch.bfloat16)
     model = sch.model
+    pool_copy = sch.kv.kv_data[0].clone()  # the timed appends overwrite cached slots
     us = time_us(lambda: rope_append_paged_kv_cache(qkv, hq, hkv, sch.d_pos[:B], model.cos, model.sin,
-                                                    sch.d_batch[:B], sch.d_pos[:B], sch.kv.kv_data[0],
+                                                    sch.d_batch[:B], sch.d_pos[:B], pool_copy,
                                                     sch.d_indices, sch.d_indptr[: B + 1], sch.d_last[:B]), 200)
     res["rope_append_decode"] = {"us": round(us, 2), "rows": B}
     # sampler: the batch's settings (half greedy, half T=0.7 / top-p 0.9)
@@ -154,6 +158,8 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--attn-iters", type=int, default=20)
+    ap.add_argument("--decode-window", type=int, default=8,
+                    help="decode steps per host round trip (1 = read the ids back after every step)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device-to-device copy (5x): the known-traffic kernel used "
@@ -185,7 +191,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     cfg = PRESETS[args.model]
     B = args.batch
-    new_tokens = max(50, args.warmup + args.steps + 1)
+    # prefill token + first decode step + warmup + two timed legs, plus slack
+    new_tokens = max(50, 2 + args.warmup + 2 * args.steps + 2)
     g = torch.Generator().manual_seed(args.seed)
     lens = torch.randint(128, 1025, (B,), generator=g).tolist()
     prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist() for n in lens]
@@ -196,31 +203,42 @@ def main() -> int:
     model = Model(cfg, dev, seed=args.seed, max_positions=max_seq + 16)
     torch.cuda.synchronize()
     log(f"weights {model.weight_bytes() / 1e9:.2f} GB in {time.time() - t0:.1f}s; capturing graphs")
-    sch = Scheduler(model, max_batch_size=B, max_seq_len=max_seq, seed=args.seed)
+    sch = Scheduler(model, max_batch_size=B, max_seq_len=max_seq, seed=args.seed, decode_window=args.decode_window)
     reqs = [Request(str(i), p, new_tokens, 0.0 if i % 2 == 0 else 0.7, 1.0 if i % 2 == 0 else 0.9)
             for i, p in enumerate(prompts)]
     for r in reqs:
         sch.submit(r)
     t0 = time.time()
+    sch.decode_window = 1
     sch.step()  # admit + ragged prefill of all 32 prompts + first decode step
     torch.cuda.synchronize()
+    def decode_steps(n: int, window: int) -> float:
+        """Exactly ``n`` decode steps in windows of ``window``; wall seconds."""
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        done = 0
+        while done < n:
+            sch.decode_window = min(window, n - done)
+            before = len(reqs[0].generated_tokens)
+            sch.step()
+            if len(reqs[0].generated_tokens) == before:
+                raise RuntimeError("no decode progress (requests finished?)")
+            done += len(reqs[0].generated_tokens) - before
+        torch.cuda.synchronize()
+        return time.perf_counter() - t
+
     log(f"prefill + first decode step {time.time() - t0:.2f}s; warmup {args.warmup} steps")
-    for _ in range(args.warmup):
-        sch.step()
-    torch.cuda.synchronize()
+    decode_steps(args.warmup, args.decode_window)
     n_active = sum(1 for r in reqs if r.status.value == "decoding")
     if n_active != B:
         raise RuntimeError(f"expected {B} decoding requests, have {n_active}")
-    log(f"timing {args.steps} decode steps at B={B}")
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        sch.step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    log(f"timing {args.steps} decode steps at B={B}, {args.decode_window} steps per host round trip")
+    elapsed = decode_steps(args.steps, args.decode_window)
     toks = B * args.steps / elapsed
     ms_step = elapsed * 1000 / args.steps
     log(f"decode: {toks:.0f} tok/s, {ms_step:.3f} ms/step")
+    if any(r.status.value != "decoding" for r in reqs):
+        raise RuntimeError("a request finished inside the timed steps")
 
     # ---------------- decode-attention kernel on the batch's real state
     hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
@@ -297,6 +315,11 @@ def main() -> int:
                          f"{med * 1000:.1f} ms per layer"}
         log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
 
+    # the same decode with the ids read back after every step (continues the batch)
+    single = decode_steps(args.steps, 1)
+    toks_single = B * args.steps / single
+    log(f"decode, one step per round trip: {toks_single:.0f} tok/s, {single * 1000 / args.steps:.3f} ms/step")
+
     mean_ctx = round(sum(kv_lens) / B, 1)
     traffic = measured_traffic(args.model, B, mean_ctx)
     line = {
@@ -313,8 +336,11 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (random-init weights, random prompt token ids)",
         "config": {"workload": f"{args.model} decode, B={B}, prompts U[128,1024] seed {args.seed}, "
-                               f"half greedy / half T=0.7 top-p 0.9, page_size 16, hipGraph decode",
-                   "batch": B, "mean_context": mean_ctx, "parallelism": "single GPU"},
+                               f"half greedy / half T=0.7 top-p 0.9, page_size 16, hipGraph decode, "
+                               f"{args.decode_window} decode steps per host round trip",
+                   "batch": B, "mean_context": mean_ctx, "decode_window": args.decode_window,
+                   "parallelism": "single GPU"},
+        "decode_tok_s_one_step_per_round_trip": round(toks_single, 2),
         "decode_attn_us": round(attn_us, 3),
         "decode_attn_gbps": round(achieved, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",

@@ -87,7 +87,7 @@ class _Pinned:
 class Scheduler:
     def __init__(self, model: Model, max_batch_size: int = 8, max_seq_len: int = 4096, page_size: int = 16,
                  num_pages: int | None = None, eos_token_ids: set[int] | None = None, use_graphs: bool = True,
-                 seed: int = 0, workspace_mb: int = 128, zero_released_pages: bool = True):
+                 seed: int = 0, workspace_mb: int = 128, zero_released_pages: bool = True, decode_window: int = 1):
         cfg = model.cfg
         self.model = model
         self.device = model.device
@@ -95,6 +95,9 @@ class Scheduler:
         self.max_batch_size = max_batch_size
         self.max_seq_len = max_seq_len
         self.eos = set(eos_token_ids or ())
+        if decode_window < 1:
+            raise ValueError("decode_window must be >= 1")
+        self.decode_window = decode_window
         self.zero_released = zero_released_pages
         self.kv = PagedKVCache(cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim, max_batch_size,
                                max_seq_len, page_size, self.device, max_num_pages=num_pages)
@@ -126,6 +129,11 @@ class Scheduler:
         self._up_t = _Pinned(bmax, torch.float32)
         self._up_p = _Pinned(bmax, torch.float32)
         self._tok_host = torch.zeros(max(bmax, max_batch_size), dtype=torch.int64).pin_memory()
+        # decode window: sampled ids of every step of the window and, per row,
+        # the first step whose id is an end-of-sequence id (computed on the GPU)
+        self.d_ring = torch.zeros(decode_window, bmax, dtype=torch.int64, device=dev)
+        self.d_eos = torch.tensor(sorted(self.eos) or [-1], dtype=torch.int64, device=dev)
+        self._ring_host = torch.zeros(decode_window + 1, bmax, dtype=torch.int64).pin_memory()
         self.waiting: deque[Request] = deque()
         self.active: list[Request] = []
         self.free_slots: deque[int] = deque(range(max_batch_size))
@@ -254,37 +262,71 @@ class Scheduler:
         return out
 
     def _decode(self, reqs: list[Request]) -> list[tuple[Request, int]]:
+        """Decode W = min(decode_window, tokens any request may still take)
+        steps with one host round trip.  Within the window the sampled ids are
+        fed back on the GPU (scheduler.py:962-978 does it on the host per
+        step), each step's page-table step and plan run ahead without waiting,
+        and end-of-sequence detection runs on the GPU over the window's ids.
+        A row that samples an end-of-sequence id keeps decoding to the end of
+        the window (its extra tokens are dropped, its pages freed at retire)."""
         b = len(reqs)
         bs = next((g for g in self.graph_sizes if g >= b), None)
         graph = self.graphs.get(bs) if bs is not None else None
         padded = bs if graph is not None else b
         if padded > self.d_batch.numel():
             raise RuntimeError(f"decode batch {b} exceeds the static buffers ({self.d_batch.numel()})")
-        rows = [(r.slot, r.current_position) for r in reqs]
-        released = self.pt.step([], rows, padded, self.d_indptr, self.d_indices, self.d_last, self.d_batch,
-                                self.d_pos)
-        self._zero_released(released)
-        self._up_ids.upload([r.generated_tokens[-1] for r in reqs] + [0] * (padded - b), self.d_ids)
+        w = min([self.decode_window] + [r.max_new_tokens - len(r.generated_tokens) for r in reqs]
+                + [self.max_seq_len - r.current_position for r in reqs])
+        w = max(1, w)
         self._up_t.upload([r.temperature for r in reqs] + [0.0] * (padded - b), self.sampler.temperature)
         self._up_p.upload([r.top_p for r in reqs] + [1.0] * (padded - b), self.sampler.top_p)
-        self._plan_decode(padded)
-        if graph is not None:
-            g, out = graph
-            g.replay()
-            toks = out
+        for j in range(w):
+            rows = [(r.slot, r.current_position + j) for r in reqs]
+            released = self.pt.step([], rows, padded, self.d_indptr, self.d_indices, self.d_last, self.d_batch,
+                                    self.d_pos)
+            self._zero_released(released)
+            if j == 0:
+                self._up_ids.upload([r.generated_tokens[-1] for r in reqs] + [0] * (padded - b), self.d_ids)
+            else:
+                self.d_ids[:padded].copy_(toks[:padded])
+            self._plan_decode(padded)
+            if graph is not None:
+                g, out = graph
+                g.replay()
+                toks = out
+            else:
+                toks = self._decode_forward(padded)
+            if w > 1:
+                self.d_ring[j, :padded].copy_(toks[:padded])
+        if w == 1:
+            host_rows = [[t] for t in self._fetch(toks, b)]
+            stops = [0 if row[0] in self.eos else 1 for row in host_rows]
         else:
-            toks = self._decode_forward(padded)
-        host = self._fetch(toks, b)
+            ring = self.d_ring[:w, :b]
+            hit = torch.isin(ring, self.d_eos)
+            first = torch.where(hit.any(0), hit.to(torch.int8).argmax(0), torch.full_like(ring[0], w))
+            self._ring_host[:w, :b].copy_(ring, non_blocking=True)
+            self._ring_host[w, :b].copy_(first, non_blocking=True)
+            torch.cuda.current_stream(self.device).synchronize()
+            host = self._ring_host[: w + 1, :b].tolist()
+            host_rows = [[host[j][i] for j in range(w)] for i in range(b)]
+            stops = host[w]
         now = time.perf_counter()
         out_list = []
-        for r, t in zip(reqs, host):
-            r.generated_tokens.append(t)
-            r.current_position += 1
-            r.last_token_time = now
-            out_list.append((r, t))
-            if t in self.eos or len(r.generated_tokens) >= r.max_new_tokens or r.current_position >= self.max_seq_len:
-                r.status = RequestStatus.FINISHED
-                r.finish_reason = "stop" if t in self.eos else "length"
+        for i, r in enumerate(reqs):
+            take = min(w, stops[i] + 1) if stops[i] < w else w
+            for t in host_rows[i][:take]:
+                r.generated_tokens.append(t)
+                r.current_position += 1
+                r.last_token_time = now
+                out_list.append((r, t))
+                if t in self.eos or len(r.generated_tokens) >= r.max_new_tokens or \
+                        r.current_position >= self.max_seq_len:
+                    r.status = RequestStatus.FINISHED
+                    r.finish_reason = "stop" if t in self.eos else "length"
+                    break
+            if r.status != RequestStatus.FINISHED and take < w:
+                raise AssertionError("decode window stopped early without an end-of-sequence id")
         return out_list
 
     def _fetch(self, toks: torch.Tensor, n: int) -> list[int]:

@@ -139,3 +139,75 @@ def test_prefill_logits_match_dense_torch(dev):
         rel = (got[i] - ref[0]).abs().max().item() / ref.abs().max().item()
         assert rel < 2e-2, rel
     assert got.shape == (3, cfg.vocab_size)
+
+
+def _run_window(model, prompts, max_new, window, eos=(), max_seq_len=1024, use_graphs=True):
+    """All prompts submitted at once; even requests greedy, odd ones
+    T=0.7 / top-p 0.9.  Returns (tokens, finish reasons, scheduler)."""
+    from minimal_inference_amd.engine import Request, Scheduler
+
+    sch = Scheduler(model, max_batch_size=8, max_seq_len=max_seq_len, use_graphs=use_graphs, seed=5,
+                    eos_token_ids=set(eos), decode_window=window)
+    reqs = [Request(str(i), p, max_new[i], 0.0 if i % 2 == 0 else 0.7, 1.0 if i % 2 == 0 else 0.9)
+            for i, p in enumerate(prompts)]
+    for r in reqs:
+        sch.submit(r)
+    n = 0
+    while sch.has_work():
+        sch.step()
+        n += 1
+        assert n < 1000
+    assert sch.pt.error_word() == 0
+    assert sch.pt.free_count == sch.kv.max_num_pages - 1
+    return [r.generated_tokens for r in reqs], [r.finish_reason for r in reqs], sch
+
+
+@pytest.mark.parametrize("window", [3, 4])
+def test_decode_window_matches_single_steps(dev, window):
+    """A decode window of W steps per host round trip (ids fed back on the
+    GPU) yields the same tokens as one step per round trip, greedy and
+    sampled rows alike; the windows shrink so that length limits (per-request
+    max_new_tokens and max_seq_len) end exactly where single steps end."""
+    model = _qwen05(dev, layers=4)
+    prompts, _ = _workload(seed=4, n=6)
+    prompts[5] = (prompts[5] * 10)[:280]
+    max_new = [20, 13, 7, 26, 9, 64]   # request 5 stops at max_seq_len 300: 1 + 20 tokens
+    ref, ref_fin, _ = _run_window(model, prompts, max_new, 1, max_seq_len=300)
+    got, fin, _ = _run_window(model, prompts, max_new, window, max_seq_len=300)
+    assert got == ref
+    assert fin == ref_fin
+    assert [len(t) for t in got] == max_new[:5] + [21]
+
+
+def test_decode_window_end_of_sequence(dev):
+    """An end-of-sequence id sampled inside a window ends its request at that
+    token (later ids of the window are dropped); the other requests are
+    unchanged up to the end of that window, when the batch first differs
+    from single-step decoding."""
+    model = _qwen05(dev, layers=4)
+    prompts, _ = _workload(seed=6, n=6)
+    max_new = [24] * 6
+    ref, _, _ = _run_window(model, prompts, max_new, 1)
+    # an id that first appears at index k >= 2 of one request and in no other request
+    pick = None
+    for i, toks in enumerate(ref):
+        for k in range(2, len(toks)):
+            t = toks[k]
+            if t in toks[:k] or any(t in o for j, o in enumerate(ref) if j != i):
+                continue
+            if k % 4 != 0:        # not the last step of its window: some steps run past it
+                pick = (i, k, t)
+                break
+        if pick:
+            break
+    assert pick is not None, "no usable end-of-sequence candidate in the trajectories"
+    i, k, eos = pick
+    got, fin, _ = _run_window(model, prompts, max_new, 4, eos=[eos])
+    assert got[i] == ref[i][: k + 1]
+    assert fin[i] == "stop"
+    same = 1 + 4 * math.ceil(k / 4)      # prefill token + every window up to the one holding the stop
+    for j in range(len(ref)):
+        if j == i:
+            continue
+        assert got[j][:same] == ref[j][:same]
+        assert fin[j] == ("stop" if eos in got[j] else "length")
