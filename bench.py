@@ -32,6 +32,13 @@ workload (same model, batch and mean context); otherwise null.
 ``cpu_baseline`` times the CPU oracle's gather-based attention on one layer of
 the same batch.
 
+``served`` reproduces the reference's published serving measurement
+(README.md:50-70, benchmark.py): the OpenAI-compatible server in a child
+process (random weights, synthetic tokenizer) and the streaming client at 2,
+20 and 32 concurrent greedy requests, max_tokens 50, 3 runs each: TTFT, T2T
+and aggregate tok/s (content chunks / run wall time, prefill included) --
+the figures the reference's 1,532 tok/s at 32 concurrent is quoted as.
+
 ``path_kernels`` times the other kernels of the path on the same state, each
 as repeated launches captured in one hipGraph and replayed between HIP events: the ragged
 causal prefill attention of the 32 prompts for one layer (MFMA bound:
@@ -135,6 +142,75 @@ def path_kernel_times(sch, cfg, reqs, lens, dev) -> dict:
     return res
 
 
+def served_leg(model: str, concurrency=(2, 20, 32), max_tokens: int = 50, runs: int = 3) -> dict:
+    """The reference's serving benchmark (README.md:50-70): the OpenAI server
+    (minimal-inference_amd/server.py, random weights of ``model``, synthetic
+    tokenizer, max_batch_size 40, max_seq_len 4096, page_size 16) runs in a
+    child process; the streaming client sends ``n`` concurrent greedy requests
+    of the prompt "Write a short poem about the ocean" with max_tokens 50,
+    ``runs`` times per ``n``, and reports mean TTFT, mean T2T and aggregate tok/s."""
+    import asyncio
+    import socket
+    import subprocess
+    import tempfile
+    import urllib.request
+
+    import yaml
+
+    from minimal_inference_amd.benchmark import run_benchmark
+
+    with socket.socket() as sk:
+        sk.bind(("127.0.0.1", 0))
+        port = sk.getsockname()[1]
+    tmp = Path(tempfile.mkdtemp(prefix="mi_served_"))
+    cfg = {"model_preset": model, "device": "cuda", "dtype": "bfloat16", "seed": 0,
+           "server": {"host": "127.0.0.1", "port": port},
+           "scheduler": {"max_seq_len": 4096, "max_batch_size": 40, "page_size": 16, "decode_window": 1,
+                         "use_graphs": True}}
+    (tmp / "server.yaml").write_text(yaml.safe_dump(cfg))
+    logf = open(tmp / "server.log", "w")
+    proc = subprocess.Popen([sys.executable, "-u", str(ROOT / "minimal-inference_amd" / "server.py"),
+                             "--config", str(tmp / "server.yaml")], stdout=logf, stderr=subprocess.STDOUT)
+    url = f"http://127.0.0.1:{port}"
+    out = {"server": f"{model} random weights, synthetic byte tokenizer, max_batch_size 40, max_seq_len 4096, "
+                     f"page_size 16, one decode step per host round trip",
+           "prompt": "Write a short poem about the ocean", "max_tokens": max_tokens, "temperature": 0, "runs": runs}
+    try:
+        t0 = time.time()
+        while True:
+            if proc.poll() is not None:
+                raise RuntimeError(f"server exited with {proc.returncode}")
+            try:
+                with urllib.request.urlopen(url + "/health", timeout=2) as r:
+                    if r.status == 200:
+                        break
+            except OSError:
+                pass
+            if time.time() - t0 > 240:
+                raise RuntimeError("server did not come up in 240 s")
+            time.sleep(0.5)
+        log(f"served: server up in {time.time() - t0:.1f}s")
+        for n in concurrency:
+            res = asyncio.run(run_benchmark(url, prompt=out["prompt"], max_tokens=max_tokens, batch_size=n,
+                                            runs=runs, verbose=False))
+            out[f"concurrent_{n}"] = {"ttft_ms": round(res["ttft_ms"], 1), "t2t_ms": round(res["t2t_ms"], 2),
+                                      "aggregate_tok_s": round(res["aggregate_tok_s"], 1)}
+            log(f"served: {n} concurrent: {out[f'concurrent_{n}']}")
+    except Exception as e:  # reported in the line, never fatal for the kernel figures
+        out["error"] = repr(e)
+        logf.flush()
+        log("served leg failed: " + repr(e) + "; server log tail:\n" + (tmp / "server.log").read_text()[-2000:])
+    finally:
+        proc.terminate()
+        try:
+            proc.wait(30)
+        except subprocess.TimeoutExpired:
+            proc.kill()
+            proc.wait()
+        logf.close()
+    return out
+
+
 def measured_traffic(model: str, batch: int, mean_context: float):
     """HBM bytes per attention launch from the committed counter summary, or
     None when it was measured on another workload."""
@@ -161,6 +237,7 @@ def main() -> int:
     ap.add_argument("--decode-window", type=int, default=8,
                     help="decode steps per host round trip (1 = read the ids back after every step)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-served", action="store_true", help="skip the HTTP serving leg")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device-to-device copy (5x): the known-traffic kernel used "
                          "to scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -320,6 +397,11 @@ def main() -> int:
     toks_single = B * args.steps / single
     log(f"decode, one step per round trip: {toks_single:.0f} tok/s, {single * 1000 / args.steps:.3f} ms/step")
 
+    served = None
+    if not args.no_served:
+        log("served leg: OpenAI server in a child process + streaming client")
+        served = served_leg(args.model)
+
     mean_ctx = round(sum(kv_lens) / B, 1)
     traffic = measured_traffic(args.model, B, mean_ctx)
     line = {
@@ -347,6 +429,7 @@ def main() -> int:
                      "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic},
         "cpu_baseline": cpu,
         "path_kernels": path,
+        "served": served,
     }
     print(json.dumps(line), flush=True)
     return 0

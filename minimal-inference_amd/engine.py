@@ -22,16 +22,26 @@ What changes (the north star's items):
 
 Per decode step the host performs one small host->device copy of op lists and
 input ids, launches the page-table kernel, ``plan()`` and the graph, and
-waits once for the sampled ids (needed to stream tokens and detect EOS).
+waits once for the sampled ids (needed to stream tokens and detect EOS) --
+or once per window of ``decode_window`` steps (see ``_decode``).
+
+Serving: ``start()`` runs the step loop in a daemon thread and
+``submit_request()`` hands requests to it from any thread
+(scheduler.py:569-604); every token, then ``None`` once the request is
+retired, goes to the request's ``sink`` (scheduler.py:1005-1009 pushes them
+into the request's asyncio queue).
 """
 
 from __future__ import annotations
 
 import enum
+import logging
 import math
+import threading
 import time
 from collections import deque
 from dataclasses import dataclass, field
+from typing import Callable
 
 import torch
 
@@ -65,6 +75,8 @@ class Request:
     finish_reason: str | None = None
     prefill_done_time: float = 0.0
     last_token_time: float = 0.0
+    # receives each token id, then None when the request is retired
+    sink: Callable[[int | None], None] | None = None
 
 
 class _Pinned:
@@ -139,6 +151,13 @@ class Scheduler:
         self.free_slots: deque[int] = deque(range(max_batch_size))
         self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
         self.steps = 0
+        # background loop state
+        self._inbox: list[Request] = []
+        self._lock = threading.Lock()
+        self._wake = threading.Event()
+        self._running = False
+        self._thread: threading.Thread | None = None
+        self.loop_error: BaseException | None = None
         if use_graphs:
             self._capture_graphs()
 
@@ -154,6 +173,65 @@ class Scheduler:
         while self.has_work() and (max_steps is None or n < max_steps):
             self.step()
             n += 1
+
+    # ------------------------------------------------------------------ background loop
+    def start(self) -> None:
+        """Run the step loop in a daemon thread (scheduler.py:569-572)."""
+        if self._thread is not None:
+            raise RuntimeError("scheduler loop already started")
+        self._running = True
+        self._thread = threading.Thread(target=self._run_loop, name="mi-scheduler", daemon=True)
+        self._thread.start()
+
+    def stop(self) -> None:
+        self._running = False
+        self._wake.set()
+        if self._thread is not None:
+            self._thread.join()
+            self._thread = None
+
+    def submit_request(self, req: Request) -> None:
+        """Thread-safe submit for a running loop (scheduler.py:580-584)."""
+        if self.loop_error is not None:
+            raise RuntimeError("scheduler loop stopped after an error") from self.loop_error
+        n = len(req.input_ids)
+        if n == 0 or n > self.max_seq_len:
+            raise ValueError(f"prompt of {n} tokens (allowed 1..{self.max_seq_len})")
+        if self.pt.pages_needed(n) > self.pt.num_pages - 1:
+            raise ValueError(f"prompt of {n} tokens needs more pages than the pool holds")
+        with self._lock:
+            self._inbox.append(req)
+        self._wake.set()
+
+    def _run_loop(self) -> None:
+        torch.cuda.set_device(self.device)
+        while self._running:
+            with self._lock:
+                new, self._inbox = self._inbox, []
+            for r in new:
+                self.submit(r)
+            if not self.has_work():
+                self._wake.wait(timeout=0.1)
+                self._wake.clear()
+                continue
+            try:
+                self.step()
+            except BaseException as e:  # fail every request, then stop
+                logging.getLogger(__name__).exception("scheduler step failed")
+                self.loop_error = e
+                with self._lock:
+                    pending, self._inbox = self._inbox, []
+                for r in list(self.active) + list(self.waiting) + pending:
+                    r.status = RequestStatus.FINISHED
+                    r.finish_reason = "error"
+                    self._push_token(r, None)
+                self.active, self.waiting = [], deque()
+                self._running = False
+
+    @staticmethod
+    def _push_token(req: Request, token: int | None) -> None:
+        if req.sink is not None:
+            req.sink(token)
 
     # ------------------------------------------------------------------ graphs
     def _backend(self, wrapper, mode, indptr, indices, last, batch, pos):
@@ -197,6 +275,8 @@ class Scheduler:
         decoding = [r for r in self.active if r.status == RequestStatus.DECODING]
         if decoding:
             emitted += self._decode(decoding)
+        for r, t in emitted:
+            self._push_token(r, t)
         self._retire()
         self.steps += 1
         return emitted
@@ -340,6 +420,7 @@ class Scheduler:
             if r.status == RequestStatus.FINISHED:
                 self.pt.release(r.slot)
                 self.free_slots.append(r.slot)
+                self._push_token(r, None)
             else:
                 still.append(r)
         self.active = still
