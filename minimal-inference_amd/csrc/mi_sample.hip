@@ -8,7 +8,10 @@
 //     (331-336).  top-p (an extension) keeps the smallest set of most likely
 //     tokens whose mass reaches top_p, ties at the boundary included.
 //
-// One 1024-thread workgroup per row.  The draw is an exponential race
+// One 1024-thread workgroup per row.  Rows of up to 40,960 tokens are read
+// once: the 16-bit keys of the scaled logits go to LDS, and every later pass
+// (top-p radix passes, draw) works on those; larger vocabularies re-read and
+// re-scale the row per pass.  The draw is an exponential race
 // (Gumbel-max): argmax_i (s_i * log2 e - log2(-log2 u_i)), which selects i with
 // probability proportional to exp(s_i); u_i comes from Philox4x32-10 (Salmon,
 // Moraes, Dror, Shaw, "Parallel random numbers: as easy as 1, 2, 3", SC 2011)
@@ -240,6 +243,195 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams p) {
   if (tid == 0) p.out[row] = bi < V ? bi : 0;
 }
 
+// ---------------------------------------------------------------- cached rows
+// 16-bit keys for the register cache: the bf16 order key, with NaN (either
+// sign) as 0xFFFF -- above +inf, whose key is 0xFF80 -- and 0 marking a slot
+// past the vocabulary (no bf16 value maps to 0: -inf is 0x007F).
+constexpr uint32_t kNaN16 = 0xFFFFu;
+__device__ __forceinline__ uint32_t key16(uint16_t b) {
+  const uint32_t k = bf16_key(b);
+  return k == kNaNKey ? kNaN16 : k;
+}
+
+// Keys of rows up to kCachedVocab tokens live in LDS (80 KB) next to the
+// radix bins (64 KB); one workgroup per CU either way.
+constexpr int kCachedVocab = 40960;
+
+__global__ __launch_bounds__(kThreads) void sample_cached_kernel(SampleParams p) {
+  __shared__ float bins[16 * kThreads];  // per-thread private radix bins
+  __shared__ uint2 keys[kCachedVocab / 4];  // 4 packed 16-bit keys per group
+  __shared__ float bin_tot[16];
+  __shared__ uint32_t sh_u[16];
+  __shared__ float sh_f[16];
+  __shared__ int sh_i[16];
+  __shared__ uint32_t sh_prefix;
+  __shared__ float sh_above, sh_target;
+
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const uint16_t* x = p.logits + int64_t(row) * p.stride;
+  const int V = p.vocab;
+  const int NG = (V + 3) / 4;  // 4-token groups; group g = tokens 4g .. 4g+3 (the draw's Philox counter)
+  const uint16_t tb = mi::f32_to_bf16(p.temperature[row]);
+  const float tq = mi::bf16_to_f32(tb);
+  const bool greedy = !(tq > 0.f);  // <= 0 (and NaN) is greedy
+  const float tmin = mi::bf16_to_f32(mi::f32_to_bf16(1e-6f));
+  const float tc = fmaxf(tq, tmin);
+  auto key_of = [](uint2 w, int e) -> uint32_t { return ((e < 2 ? w.x : w.y) >> (16 * (e & 1))) & 0xffffu; };
+
+  // ---- read the row once: keys of the raw logits (greedy rows) or of
+  // bf16(x / t) (sampled rows); 0 past the vocabulary.  All of a thread's
+  // loads are issued before any is used (one memory round trip).
+  const bool vec = (reinterpret_cast<uintptr_t>(x) & 7) == 0;
+  uint32_t bk = 0, mk = 0;
+  int bi = 0x7fffffff;
+  constexpr int kMaxG = kCachedVocab / 4 / kThreads;  // groups per thread
+  uint16_t raw[kMaxG][4];
+#pragma unroll
+  for (int n = 0; n < kMaxG; ++n) {
+    const int t0 = 4 * (tid + n * kThreads);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) raw[n][e] = 0;
+    if (vec && t0 + 3 < V) {
+      const uint2 w = *reinterpret_cast<const uint2*>(x + t0);
+      raw[n][0] = uint16_t(w.x);
+      raw[n][1] = uint16_t(w.x >> 16);
+      raw[n][2] = uint16_t(w.y);
+      raw[n][3] = uint16_t(w.y >> 16);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (t0 + e < V) raw[n][e] = x[t0 + e];
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < kMaxG; ++n) {
+    const int gi = tid + n * kThreads;
+    if (gi >= NG) break;
+    const int t0 = 4 * gi;
+    const uint16_t* v = raw[n];
+    uint32_t k[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t sv = greedy ? v[e] : mi::f32_to_bf16(mi::bf16_to_f32(v[e]) / tc);
+      k[e] = (t0 + e < V) ? key16(sv) : 0u;
+      if (t0 + e < V) better(bk, bi, k[e], t0 + e);
+      mk = max(mk, k[e]);
+    }
+    keys[gi] = make_uint2(k[0] | (k[1] << 16), k[2] | (k[3] << 16));
+  }
+
+  if (greedy) {
+    block_argmax<uint32_t>(bk, bi, sh_u, sh_i);
+    if (tid == 0) p.out[row] = bi < V ? bi : 0;
+    return;
+  }
+  {
+    int unused = 0;
+    block_argmax<uint32_t>(mk, unused, sh_u, sh_i);  // ends with barriers: keys[] is complete
+  }
+  const float smax = key_to_f32(mk) * mi::kLog2e;
+
+  // ---- top-p boundary key: four 4-bit radix passes over the cached keys
+  uint32_t kstar = 0;
+  const float tp = p.top_p ? p.top_p[row] : 1.0f;
+  if (tp < 1.0f && mk != kNaN16) {
+    uint32_t prefix = 0;
+    if (tid == 0) sh_above = 0.f;
+    for (int pass = 0; pass < 4; ++pass) {
+      const int shift = 12 - 4 * pass;
+#pragma unroll
+      for (int d = 0; d < 16; ++d) bins[d * kThreads + tid] = 0.f;
+      for (int gi = tid; gi < NG; gi += kThreads) {
+        const uint2 w = keys[gi];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t k = key_of(w, e);
+          if (k == 0u || (pass > 0 && (k >> (shift + 4)) != prefix)) continue;
+          const float mass = __builtin_amdgcn_exp2f(key_to_f32(k) * mi::kLog2e - smax);
+          bins[((k >> shift) & 15) * kThreads + tid] += mass;  // private bin
+        }
+      }
+      __syncthreads();
+      {
+        const int w = tid >> 6, lane = tid & 63;  // wave w sums digit w
+        float s = 0.f;
+        for (int j = lane; j < kThreads; j += 64) s += bins[w * kThreads + j];
+        s = mi::wave_sum(s);
+        if (lane == 0) bin_tot[w] = s;
+      }
+      __syncthreads();
+      if (tid < 64) {
+        // Wave 0, lane d < 16 holds digit d's mass.  The digit is the highest
+        // non-empty d whose mass together with everything above it (the
+        // masses above the current prefix, plus digits > d) reaches the
+        // target; if rounding leaves the target unreached, the lowest
+        // non-empty digit.
+        const int lane = tid;
+        const float bt = lane < 16 ? bin_tot[lane] : 0.f;
+        float target;
+        if (pass == 0) {
+          target = tp * mi::wave_sum(bt);
+          if (lane == 0) sh_target = target;
+        } else {
+          target = sh_target;
+        }
+        float c = bt;  // suffix sum over digits >= lane
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+          const float up = __shfl_down(c, o);
+          if (lane + o < 16) c += up;
+        }
+        const float above0 = sh_above;
+        const uint64_t hit = __ballot(lane < 16 && bt > 0.f && above0 + c >= target);
+        const uint64_t nonempty = __ballot(lane < 16 && bt > 0.f);
+        const int pick = hit ? 63 - __builtin_clzll(hit) : (nonempty ? __builtin_ctzll(nonempty) : 0);
+        const float c_above = __shfl(c, pick + 1);  // digits > pick (lane 16 holds 0)
+        if (lane == 0) {
+          sh_above = above0 + (pick + 1 < 16 ? c_above : 0.f);
+          sh_prefix = (prefix << 4) | uint32_t(pick);
+        }
+      }
+      __syncthreads();
+      prefix = sh_prefix;
+      __syncthreads();
+    }
+    kstar = prefix;
+  }
+
+  // ---- exponential race over the kept tokens; a group with no kept token
+  // skips its Philox block
+  const uint64_t off = *p.offset;
+  float bv = -INFINITY;
+  bi = 0x7fffffff;
+  for (int gi = tid; gi < NG; gi += kThreads) {
+    const uint2 w = keys[gi];
+    bool any = false;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) any = any || (4 * gi + e < V && key_of(w, e) >= kstar);
+    if (!any) continue;
+    const uint4 r = philox4x32_10(make_uint4(uint32_t(gi), uint32_t(row), uint32_t(off), uint32_t(off >> 32)), p.seed);
+    const uint32_t rr[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 4 * gi + e;
+      const uint32_t k = key_of(w, e);
+      if (i >= V || k < kstar) continue;
+      float v;
+      if (k == kNaN16) {
+        v = INFINITY;
+      } else {
+        const float sc = key_to_f32(k);
+        if (sc == -INFINITY) continue;
+        v = sc * mi::kLog2e - __log2f(-__log2f(u01(rr[e])));
+      }
+      betterf(bv, bi, v, i);
+    }
+  }
+  block_argmax<float>(bv, bi, sh_f, sh_i);
+  if (tid == 0) p.out[row] = bi < V ? bi : 0;
+}
+
 __global__ void advance_offset_kernel(uint64_t* off) {
   if (threadIdx.x == 0 && blockIdx.x == 0) off[0] += 1;
 }
@@ -267,7 +459,10 @@ extern "C" int mi_sample(const void* logits, int64_t logits_row_stride, int32_t 
   sp.offset = rng_offset;
   sp.out = out_tokens;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(sample_kernel, dim3(batch_size), dim3(kThreads), 0, s, sp);
+  if (vocab_size <= kCachedVocab)
+    hipLaunchKernelGGL(sample_cached_kernel, dim3(batch_size), dim3(kThreads), 0, s, sp);
+  else
+    hipLaunchKernelGGL(sample_kernel, dim3(batch_size), dim3(kThreads), 0, s, sp);
   int rc = mi::check_launch("sample_kernel");
   if (rc) return rc;
   hipLaunchKernelGGL(advance_offset_kernel, dim3(1), dim3(64), 0, s, rng_offset);
