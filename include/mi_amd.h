@@ -237,6 +237,29 @@ int mi_pages_zero(void* pools, int64_t layer_stride_bytes, int32_t num_layers,
                   int64_t num_pages, int64_t page_bytes, const int32_t* page_ids, int32_t n_pages,
                   mi_stream_t stream);
 
+/* ------------------------------------------------------------------------ *
+ * Dense-layer fusions around the attention path.
+ *
+ * mi_add_rms_norm replaces the residual add of DecoderLayer.forward
+ * (model.py:335-343) and the RMSNorm that follows it (model.py:115-122,
+ * F.rms_norm): for each of `rows` rows of `hidden` bf16 values,
+ *   x' = bf16(x + delta)           (delta may be null: x' = x)
+ *   h  = bf16(x' * rsqrt(mean(x'^2) + eps) * weight)   (fp32, one rounding)
+ * x' is written to x_out when x_out is not null (x_out may alias x); h is
+ * written when h_out is not null.  hidden: multiple of 8, <= 16384; rows and
+ * weight 16-byte aligned (element strides multiples of 8).
+ *
+ * mi_silu_mul replaces silu(gate(x)) * up(x) of the MLP (model.py:301-311)
+ * over the fused gate/up projection [rows][2 * intermediate]:
+ *   out = bf16(bf16(g / (1 + exp(-g))) * u),  g = row[j], u = row[intermediate + j].
+ * ------------------------------------------------------------------------ */
+int mi_add_rms_norm(const void* x, int64_t x_stride, const void* delta, int64_t delta_stride,
+                    const void* weight, void* x_out, int64_t x_out_stride, void* h_out,
+                    int64_t h_stride, int64_t rows, int32_t hidden, float eps, mi_stream_t stream);
+
+int mi_silu_mul(const void* gate_up, int64_t gate_up_stride, void* out, int64_t out_stride,
+                int64_t rows, int32_t intermediate, mi_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -67,6 +67,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _c_u64, _vp, _vp, _vp],
     ),
+    "mi_add_rms_norm": (
+        _c_i32,
+        [_vp, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _vp, _c_i64, _c_i64, _c_i32, _c_f32, _vp],
+    ),
+    "mi_silu_mul": (_c_i32, [_vp, _c_i64, _vp, _c_i64, _c_i64, _c_i32, _vp]),
     "mi_page_table_state_size": (_c_sz, [_c_i32, _c_i32, _c_i32]),
     "mi_page_table_init": (ctypes.c_int, [_vp, _c_i32, _c_i32, _c_i32, _vp]),
     "mi_page_table_step": (

@@ -45,6 +45,10 @@ constexpr float kLazyRescale = 8.0f;
 #ifndef PREFILL_WAVES
 #define PREFILL_WAVES 2
 #endif
+// Row blocks of 16 per wave for head_dim 64 / 128 (256: always 1).
+#ifndef PREFILL_MAXRB
+#define PREFILL_MAXRB 2
+#endif
 
 struct alignas(32) PrefillTile {
   int b;
@@ -70,7 +74,7 @@ constexpr int waves_for(int /*head_dim*/) { return 4; }
 // Query positions per workgroup: about `rows` (position, head) rows, where
 // rows = 128 for head_dim <= 128 (two row blocks per wave) and 64 for 256.
 int rows_per_tile(int group, int head_dim) {
-  const int rows = head_dim <= 128 ? 128 : 64;
+  const int rows = head_dim <= 128 ? 16 * waves_for(head_dim) * PREFILL_MAXRB : 64;
   const int bm = (rows / group) / 16 * 16;
   return bm < kMinRows ? kMinRows : bm;
 }
@@ -558,8 +562,8 @@ extern "C" int mi_prefill_run(void* workspace, size_t workspace_bytes, const voi
   const dim3 g{static_cast<uint32_t>(grid), 1u, 1u};
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (head_dim) {
-    case 64: hipLaunchKernelGGL((prefill_run_kernel<64, 2>), g, dim3(64 * waves_for(64)), 0, s, rp); break;
-    case 128: hipLaunchKernelGGL((prefill_run_kernel<128, 2>), g, dim3(64 * waves_for(128)), 0, s, rp); break;
+    case 64: hipLaunchKernelGGL((prefill_run_kernel<64, PREFILL_MAXRB>), g, dim3(64 * waves_for(64)), 0, s, rp); break;
+    case 128: hipLaunchKernelGGL((prefill_run_kernel<128, PREFILL_MAXRB>), g, dim3(64 * waves_for(128)), 0, s, rp); break;
     default: hipLaunchKernelGGL((prefill_run_kernel<256, 1>), g, dim3(64 * waves_for(256)), 0, s, rp); break;
   }
   return mi::check_launch("prefill_run_kernel");

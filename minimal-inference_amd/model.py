@@ -13,8 +13,12 @@ form): q/k/v projections are one fused GEMM and gate/up one fused GEMM, and
 prefill computes logits only for each request's last position.  By default
 RoPE on q and k and the K/V append run as one HIP launch
 (``rope_append_paged_kv_cache``), bit-identical to the reference's bf16
-RoPE ops followed by the append; ``fused_rope=False`` keeps the separate ops.  RoPE tables
-are held in the model dtype, as the reference's are after ``.to(dtype)``
+RoPE ops followed by the append; ``fused_rope=False`` keeps the separate ops.
+By default the residual adds and the RMSNorms that follow them run as one
+HIP kernel each, and SiLU(gate) * up as one (``dense.add_rms_norm`` /
+``dense.silu_mul``, fp32 math, one bf16 rounding per output);
+``fused_dense=False`` keeps torch's ``F.rms_norm``, adds and
+``F.silu(g) * u``.  RoPE tables are held in the model dtype, as the reference's are after ``.to(dtype)``
 (server.py:251).  Weights are random-initialised on the device (N(0, 0.02),
 norms 1) -- the benchmark configurations use random weights.
 """
@@ -29,6 +33,7 @@ import os
 import torch
 import torch.nn.functional as F
 
+from .dense import add_rms_norm, silu_mul
 from .page import append_paged_kv_cache, rope_append_paged_kv_cache
 
 
@@ -152,9 +157,10 @@ class AttentionBackend:
 
 class Model:
     def __init__(self, cfg: ModelConfig, device, dtype=torch.bfloat16, seed: int = 0, max_positions: int | None = None,
-                 fused_rope: bool = True):
+                 fused_rope: bool = True, fused_dense: bool = True):
         self.cfg = cfg
         self.fused_rope = fused_rope
+        self.fused_dense = fused_dense
         self.device = torch.device(device)
         self.dtype = dtype
         gen = torch.Generator(device=self.device).manual_seed(seed)
@@ -195,9 +201,14 @@ class Model:
             sin = self.sin.index_select(0, positions)
         t = input_ids.shape[0]
         backend._layer_idx = 0
-        for L in self.layers:
+        eps = cfg.rms_norm_eps
+        dense = self.fused_dense
+        if dense:
+            h = add_rms_norm(x, None, self.layers[0].in_norm, eps, write_x=False)
+        for li, L in enumerate(self.layers):
             layer_idx = backend.next_layer()
-            h = F.rms_norm(x, (cfg.hidden_size,), L.in_norm, cfg.rms_norm_eps)
+            if not dense:
+                h = F.rms_norm(x, (cfg.hidden_size,), L.in_norm, eps)
             qkv = F.linear(h, L.w_qkv, L.b_qkv)
             kv_data = backend.paged_kv_cache.kv_data[layer_idx]
             if fused:
@@ -212,15 +223,28 @@ class Model:
                 append_paged_kv_cache(k, v, backend.batch_indices, backend.positions, kv_data,
                                       backend.kv_page_indices, backend.kv_page_indptr, backend.kv_last_page_len)
             o = backend.wrapper.run(q, kv_data)
-            x = x + F.linear(o.view(t, nq * d), L.w_o)
-            h = F.rms_norm(x, (cfg.hidden_size,), L.post_norm, cfg.rms_norm_eps)
-            gu = F.linear(h, L.w_gate_up)
-            g, u = gu.chunk(2, dim=-1)
-            x = x + F.linear(F.silu(g) * u, L.w_down)
-        if last_rows is not None:
-            x = x.index_select(0, last_rows)
-        x = F.rms_norm(x, (cfg.hidden_size,), self.norm, cfg.rms_norm_eps)
-        return F.linear(x, self.lm_head)
+            if not dense:
+                x = x + F.linear(o.view(t, nq * d), L.w_o)
+                h = F.rms_norm(x, (cfg.hidden_size,), L.post_norm, eps)
+                gu = F.linear(h, L.w_gate_up)
+                g, u = gu.chunk(2, dim=-1)
+                x = x + F.linear(F.silu(g) * u, L.w_down)
+                continue
+            # x += o W_o; h = rms(x); x += down(silu(g) * u); h = next layer's rms(x)
+            h = add_rms_norm(x, F.linear(o.view(t, nq * d), L.w_o), L.post_norm, eps)
+            down = F.linear(silu_mul(F.linear(h, L.w_gate_up)), L.w_down)
+            if li + 1 < len(self.layers):
+                h = add_rms_norm(x, down, self.layers[li + 1].in_norm, eps)
+            elif last_rows is None:
+                h = add_rms_norm(x, down, self.norm, eps)
+            else:
+                add_rms_norm(x, down, None, eps, norm=False)
+                h = add_rms_norm(x.index_select(0, last_rows), None, self.norm, eps, write_x=False)
+        if not dense:
+            if last_rows is not None:
+                x = x.index_select(0, last_rows)
+            h = F.rms_norm(x, (cfg.hidden_size,), self.norm, eps)
+        return F.linear(h, self.lm_head)
 
 
 def kv_pool_bytes_per_page(cfg: ModelConfig, page_size: int = 16) -> int:
