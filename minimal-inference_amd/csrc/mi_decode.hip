@@ -52,6 +52,9 @@ constexpr int kUnitsPerCU = MI_DECODE_UNITS_PER_CU;
 #ifndef MI_DECODE_WAVES
 #define MI_DECODE_WAVES 2
 #endif
+#ifndef MI_DECODE_RS_PAD
+#define MI_DECODE_RS_PAD 16
+#endif
 #ifndef MI_DECODE_KB_REGS
 #define MI_DECODE_KB_REGS 96
 #endif
@@ -251,7 +254,7 @@ struct DecodeTraits {
   static constexpr int NT = D / 16;      // 16-wide head_dim tiles for O += P V
   static constexpr int CPR = D / 8;      // 16-byte chunks per token row of one head
   static constexpr int LPI = CPR / 4;    // 16-byte loads per lane per page, for K and for V
-  static constexpr int RS = D * 2 + 16;  // LDS row stride in bytes (16 B pad spreads the banks)
+  static constexpr int RS = D * 2 + MI_DECODE_RS_PAD;  // LDS row stride in bytes (the pad spreads the banks)
   static constexpr int SLOT = 4 * kPageSize * RS;  // two pages of K and V in LDS
   // Pages in flight per wave (~128-160 registers of staging).
   static constexpr int NB = (D == 64) ? MI_DECODE_NB64 : (D == 128) ? MI_DECODE_NB128 : 2;

