@@ -153,6 +153,7 @@ class Scheduler:
         self.steps = 0
         # background loop state
         self._inbox: list[Request] = []
+        self._aborts: set[str] = set()
         self._lock = threading.Lock()
         self._wake = threading.Event()
         self._running = False
@@ -203,13 +204,40 @@ class Scheduler:
             self._inbox.append(req)
         self._wake.set()
 
+    def abort_request(self, request_id: str) -> None:
+        """Thread-safe: stop a request of the running loop.  It finishes with
+        finish_reason "abort" (its sink gets None) and its pages are released
+        at the end of the loop's next step; unknown or finished ids are
+        ignored."""
+        with self._lock:
+            self._aborts.add(request_id)
+        self._wake.set()
+
+    def _apply_aborts(self, ids: set[str]) -> None:
+        kept = deque()
+        for r in self.waiting:
+            if r.request_id in ids:
+                r.status = RequestStatus.FINISHED
+                r.finish_reason = "abort"
+                self._push_token(r, None)
+            else:
+                kept.append(r)
+        self.waiting = kept
+        for r in self.active:
+            if r.request_id in ids and r.status != RequestStatus.FINISHED:
+                r.status = RequestStatus.FINISHED  # retired (pages released, sink closed) by the next step
+                r.finish_reason = "abort"
+
     def _run_loop(self) -> None:
         torch.cuda.set_device(self.device)
         while self._running:
             with self._lock:
                 new, self._inbox = self._inbox, []
+                aborts, self._aborts = self._aborts, set()
             for r in new:
                 self.submit(r)
+            if aborts:
+                self._apply_aborts(aborts)
             if not self.has_work():
                 self._wake.wait(timeout=0.1)
                 self._wake.clear()
@@ -358,6 +386,11 @@ class Scheduler:
         w = min([self.decode_window] + [r.max_new_tokens - len(r.generated_tokens) for r in reqs]
                 + [self.max_seq_len - r.current_position for r in reqs])
         w = max(1, w)
+        # shrink the window until the pool covers every row's growth over it
+        # (one step that does not fit raises, as allocate_pages does)
+        while w > 1 and sum(max(0, self.pt.pages_needed(r.current_position + w) - self.pt.slot_npages[r.slot])
+                            for r in reqs) > self.pt.free_count:
+            w -= 1
         self._up_t.upload([r.temperature for r in reqs] + [0.0] * (padded - b), self.sampler.temperature)
         self._up_p.upload([r.top_p for r in reqs] + [1.0] * (padded - b), self.sampler.top_p)
         for j in range(w):

@@ -7,7 +7,9 @@ non-empty text delta, a last chunk with an empty delta and the
 ``finish_reason`` ("stop" after a stop id, which is not sent as text,
 otherwise "length"), then ``data: [DONE]``.  Additions: an optional
 ``top_p`` field, ``GET /v1/models`` and ``GET /health``; prompts that can
-never fit (longer than ``max_seq_len`` or the pool) are answered with 400.
+never fit (longer than ``max_seq_len`` or the pool) are answered with 400;
+a request whose client goes away is aborted in the engine (the reference
+keeps generating for it).
 
 The engine (``engine.Scheduler``) runs its step loop in a daemon thread and
 pushes each token into the request's asyncio queue with
@@ -158,18 +160,27 @@ def create_app(scheduler, tokenizer, model_name: str, stop_ids: set[int]) -> Fas
             return StreamingResponse(_stream(req, queue, name), media_type="text/event-stream")
         return await _complete(req, queue, name)
 
+    def abort(req: Request) -> None:
+        fn = getattr(scheduler, "abort_request", None)
+        if fn is not None:
+            fn(req.request_id)
+
     async def _complete(req: Request, queue: asyncio.Queue, name: str) -> ChatCompletionResponse:
         ids: list[int] = []
         finish = "length"
-        while True:
-            t = await queue.get()
-            if t is None:
-                finish = req.finish_reason or finish
-                break
-            if t in stops:
-                finish = "stop"
-                continue
-            ids.append(t)
+        try:
+            while True:
+                t = await queue.get()
+                if t is None:
+                    finish = req.finish_reason or finish
+                    break
+                if t in stops:
+                    finish = "stop"
+                    continue
+                ids.append(t)
+        except asyncio.CancelledError:  # the client went away
+            abort(req)
+            raise
         if finish == "error":
             raise HTTPException(500, "engine error")
         return ChatCompletionResponse(
@@ -188,20 +199,26 @@ def create_app(scheduler, tokenizer, model_name: str, stop_ids: set[int]) -> Fas
                                     choices=[StreamChoice(delta=delta, finish_reason=finish)])
             return f"data: {c.model_dump_json()}\n\n"
 
-        yield chunk(DeltaMessage(role="assistant"))
-        detok = IncrementalDetokenizer(tokenizer)
-        finish = "length"
-        while True:
-            t = await queue.get()
-            if t is None:
-                finish = req.finish_reason or finish
-                break
-            if t in stops:
-                finish = "stop"
-                continue
-            text = detok.push(t)
-            if text:
-                yield chunk(DeltaMessage(content=text))
+        done = False
+        try:
+            yield chunk(DeltaMessage(role="assistant"))
+            detok = IncrementalDetokenizer(tokenizer)
+            finish = "length"
+            while True:
+                t = await queue.get()
+                if t is None:
+                    done = True
+                    finish = req.finish_reason or finish
+                    break
+                if t in stops:
+                    finish = "stop"
+                    continue
+                text = detok.push(t)
+                if text:
+                    yield chunk(DeltaMessage(content=text))
+        finally:
+            if not done:  # closed early: the client disconnected
+                abort(req)
         tail = detok.flush()
         if tail:
             yield chunk(DeltaMessage(content=tail))

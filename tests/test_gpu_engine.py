@@ -211,3 +211,31 @@ def test_decode_window_end_of_sequence(dev):
             continue
         assert got[j][:same] == ref[j][:same]
         assert fin[j] == ("stop" if eos in got[j] else "length")
+
+
+def test_decode_window_shrinks_to_free_pages(dev):
+    """The window is cut so every row's page growth over it fits the free
+    pages (here the host count is lowered to one page right before a window
+    whose 8 steps would cross a page boundary in both rows): 2 steps run
+    instead of 8, and nothing is allocated past the pool."""
+    from minimal_inference_amd.engine import Request, Scheduler
+
+    model = _qwen05(dev, layers=2)
+    sch = Scheduler(model, max_batch_size=4, max_seq_len=512, decode_window=8)
+    g = torch.Generator().manual_seed(12)
+    reqs = [Request(str(i), torch.randint(0, 151936, (30,), generator=g).tolist(), 40, 0.0) for i in range(2)]
+    for r in reqs:
+        sch.submit(r)
+    sch.step()   # prefill (position 30) + a window of 8: positions 30..37
+    sch.step()   # positions 38..45, still three pages each
+    assert [r.current_position for r in reqs] == [46, 46]
+    saved = sch.pt.free_count
+    sch.pt.free_count = 1        # the next 8 steps would need a fourth page in both rows
+    sch.step()
+    assert [r.current_position for r in reqs] == [48, 48]   # positions 46, 47 only
+    assert sch.pt.free_count == 1
+    sch.pt.free_count = saved
+    while sch.has_work():
+        sch.step()
+    assert [len(r.generated_tokens) for r in reqs] == [40, 40]
+    assert sch.pt.error_word() == 0

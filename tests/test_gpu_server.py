@@ -44,6 +44,9 @@ class _Recorder:
         self.by_id[req.request_id] = req
         self.sch.submit_request(req)
 
+    def abort_request(self, request_id):
+        self.sch.abort_request(request_id)
+
     @property
     def loop_error(self):
         return self.sch.loop_error
@@ -113,3 +116,53 @@ def test_served_streams_match_engine_tokens(dev, window):
     assert res["t2t_ms"] > 0 and res["ttft_ms"] > 0
     assert not sch.active and not sch.waiting
     assert sch.pt.free_count == sch.kv.max_num_pages - 1              # every request retired
+
+
+def test_client_disconnect_aborts_in_engine(dev):
+    """A streaming client that goes away after a few chunks: the engine
+    retires the request with finish_reason "abort" and frees its pages."""
+    import httpx
+    import uvicorn
+
+    from minimal_inference_amd.engine import Scheduler
+    from minimal_inference_amd.model import PRESETS, Model
+    from minimal_inference_amd.server import create_app
+    from minimal_inference_amd.tokenizer import SyntheticTokenizer, stop_ids
+
+    cfg = PRESETS["qwen2.5-0.5b"]
+    model = Model(cfg, dev, seed=7, max_positions=4200)   # 24 layers: ~1 ms per step, 3000 tokens take seconds
+    tok = SyntheticTokenizer(cfg.vocab_size)
+    stops = stop_ids(tok)
+    sch = Scheduler(model, max_batch_size=4, max_seq_len=4096, eos_token_ids=stops, seed=0)
+    rec = _Recorder(sch)
+    sch.start()
+    port = _free_port()
+    server = uvicorn.Server(uvicorn.Config(create_app(rec, tok, "qwen-test", stops), host="127.0.0.1", port=port,
+                                           log_level="warning"))
+    th = threading.Thread(target=server.run, daemon=True)
+    th.start()
+    try:
+        t0 = time.time()
+        while not server.started:
+            assert time.time() - t0 < 30
+            time.sleep(0.05)
+        body = {"messages": [{"role": "user", "content": PROMPT}], "max_tokens": 3000, "temperature": 0,
+                "stream": True}
+        with httpx.stream("POST", f"http://127.0.0.1:{port}/v1/chat/completions", json=body, timeout=60) as r:
+            n = 0
+            for line in r.iter_lines():
+                n += line.startswith("data: ")
+                if n >= 5:
+                    break
+        t0 = time.time()
+        while (sch.active or sch.waiting) and time.time() - t0 < 20:
+            time.sleep(0.05)
+    finally:
+        server.should_exit = True
+        th.join(15)
+        sch.stop()
+    (req,) = rec.by_id.values()
+    assert req.finish_reason == "abort"
+    assert len(req.generated_tokens) < 3000
+    assert not sch.active and not sch.waiting
+    assert sch.pt.free_count == sch.kv.max_num_pages - 1

@@ -30,9 +30,14 @@ class FakeScheduler:
 
     max_seq_len = 256
 
-    def __init__(self, script):
+    def __init__(self, script, delay=0.002):
         self.script = list(script)
+        self.delay = delay
         self.requests = []
+        self.aborted = set()
+
+    def abort_request(self, request_id):
+        self.aborted.add(request_id)
 
     def submit_request(self, req):
         if len(req.input_ids) > self.max_seq_len:
@@ -42,9 +47,13 @@ class FakeScheduler:
         def run():
             out = []
             for t in self.script:
+                if req.request_id in self.aborted:
+                    req.finish_reason = "abort"
+                    req.sink(None)
+                    return
                 out.append(t)
                 req.sink(t)
-                time.sleep(0.002)
+                time.sleep(self.delay)
                 if t == EOS or len(out) >= req.max_new_tokens:
                     break
             req.finish_reason = "stop" if out and out[-1] == EOS else "length"
@@ -53,11 +62,11 @@ class FakeScheduler:
         threading.Thread(target=run, daemon=True).start()
 
 
-def _app(script):
+def _app(script, delay=0.002):
     from minimal_inference_amd.server import create_app
 
     tok = SyntheticTokenizer(VOCAB)
-    sch = FakeScheduler(script)
+    sch = FakeScheduler(script, delay)
     return create_app(sch, tok, "fake-model", {EOS}), sch, tok
 
 
@@ -287,3 +296,36 @@ def test_load_weights_hf_layout(tmp_path):
     save_file(sd, str(tmp_path / "model.safetensors"))
     with pytest.raises(ValueError, match="lacks 1 tensors"):
         load_weights(Model(cfg, "cpu", seed=1, max_positions=64), str(tmp_path))
+
+
+def test_client_disconnect_aborts_request():
+    """A streaming client that closes after a few chunks gets its request
+    aborted in the engine (the scheduler's abort_request is called)."""
+    import httpx
+    import uvicorn
+
+    app, sch, _ = _app([300 + i for i in range(200)], delay=0.02)
+    port = _free_port()
+    server = uvicorn.Server(uvicorn.Config(app, host="127.0.0.1", port=port, log_level="warning"))
+    th = threading.Thread(target=server.run, daemon=True)
+    th.start()
+    try:
+        t0 = time.time()
+        while not server.started:
+            assert time.time() - t0 < 20
+            time.sleep(0.05)
+        body = {"messages": [{"role": "user", "content": "hi"}], "max_tokens": 200, "stream": True}
+        with httpx.stream("POST", f"http://127.0.0.1:{port}/v1/chat/completions", json=body, timeout=30) as r:
+            n = 0
+            for line in r.iter_lines():
+                if line.startswith("data: "):
+                    n += 1
+                if n >= 4:
+                    break
+        t0 = time.time()
+        while not sch.aborted and time.time() - t0 < 10:
+            time.sleep(0.05)
+    finally:
+        server.should_exit = True
+        th.join(10)
+    assert sch.aborted == {sch.requests[0].request_id}
