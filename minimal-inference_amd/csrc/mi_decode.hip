@@ -182,10 +182,16 @@ __device__ int block_inclusive_scan(int v, int* buf, int* total) {
 __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
   __shared__ int red[16];
   __shared__ int scan[1024];
+  __shared__ int s_np[1024], s_pb0[1024], s_lpl[1024];
   const int t = threadIdx.x;
-  int mx = 0;
-  for (int b = t; b < p.batch; b += blockDim.x) mx = max(mx, p.indptr[b + 1] - p.indptr[b]);
+  int mx = 0, tot = 0;
+  for (int b = t; b < p.batch; b += blockDim.x) {
+    const int np = max(0, p.indptr[b + 1] - p.indptr[b]);
+    mx = max(mx, np);
+    tot += np;
+  }
   const int max_np = block_max(mx, red);
+  const long long total_np = block_sum(tot, red);
   // Pages per item ("chunk"): the smallest value whose items fit the limit,
   // found by binary search (the item count is non-increasing in chunk).  The
   // limit is one resident round of units (target_units / kv_heads items), so
@@ -194,7 +200,10 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
   const int round_items = max(1, p.target_units / p.hkv);
   int limit = ((p.batch + round_items - 1) / round_items) * round_items;
   limit = min(max(limit, 1), p.max_items);
-  int lo = 1, hi = max(max_np, 1);
+  // every chunk below total / limit has more than `limit` items (each
+  // request has at least ceil(np / chunk) of them)
+  int hi = max(max_np, 1);
+  int lo = min(hi, max(1, int((total_np + limit - 1) / limit)));
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
     int cnt = 0;
@@ -205,37 +214,52 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
     if (block_sum(cnt, red) <= limit) hi = mid; else lo = mid + 1;
   }
   const int chunk = lo;
+  // Items, 1024 requests at a time: the scan gives each request's first
+  // item, then every thread writes whole items (one item per thread per
+  // round, its inline page ids loaded together), finding the item's request
+  // by binary search over the scan.
   int running = 0;
   for (int base = 0; base < p.batch; base += blockDim.x) {
     const int b = base + t;
-    int np = 0, ns = 0;
+    int np = 0, ns = 0, pb0 = 0, lpl = 1;
     if (b < p.batch) {
-      np = max(0, p.indptr[b + 1] - p.indptr[b]);
+      pb0 = p.indptr[b];
+      np = max(0, p.indptr[b + 1] - pb0);
       ns = max(1, (np + chunk - 1) / chunk);
+      lpl = min(max(p.last_page_len[b], 1), kPageSize);
     }
+    s_np[t] = np;
+    s_pb0[t] = pb0;
+    s_lpl[t] = lpl;
     int chunk_total = 0;
-    const int incl = block_inclusive_scan(ns, scan, &chunk_total);
-    const int first = running + incl - ns;
-    if (b < p.batch && first + ns <= p.max_items) {
-      int lpl = p.last_page_len[b];
-      lpl = min(max(lpl, 1), kPageSize);
-      const int pb0 = p.indptr[b];
-      for (int s = 0; s < ns; ++s) {
-        DecodeItem it;
-        it.b = b;
-        it.page_begin = pb0 + int((long long)s * np / ns);
-        it.page_end = pb0 + int((long long)(s + 1) * np / ns);
-        it.last_valid = (np == 0) ? 0 : (s == ns - 1 ? lpl : kPageSize);
-        it.split = s;
-        it.nsplit = ns;
-        it.item_base = first;
-        it.pad = 0;
-        for (int j = 0; j < kInlinePages; ++j)
-          it.pages[j] = (it.page_begin + j < it.page_end) ? p.indices[it.page_begin + j] : -1;
-        p.items[first + s] = it;
+    block_inclusive_scan(ns, scan, &chunk_total);  // its barriers also publish s_np / s_pb0 / s_lpl
+    for (int idx = t; idx < chunk_total; idx += blockDim.x) {
+      int lo_r = 0, hi_r = int(blockDim.x) - 1;  // request r: the first with scan[r] > idx
+      while (lo_r < hi_r) {
+        const int mid = (lo_r + hi_r) >> 1;
+        if (scan[mid] > idx) hi_r = mid; else lo_r = mid + 1;
       }
+      const int r = lo_r;
+      const int nsr = scan[r] - (r > 0 ? scan[r - 1] : 0);
+      const int first = running + scan[r] - nsr;
+      if (first + nsr > p.max_items) continue;  // the request does not fit: none of its items
+      const int sp = idx - (scan[r] - nsr);
+      const int npr = s_np[r];
+      DecodeItem it;
+      it.b = base + r;
+      it.page_begin = s_pb0[r] + int((long long)sp * npr / nsr);
+      it.page_end = s_pb0[r] + int((long long)(sp + 1) * npr / nsr);
+      it.last_valid = (npr == 0) ? 0 : (sp == nsr - 1 ? s_lpl[r] : kPageSize);
+      it.split = sp;
+      it.nsplit = nsr;
+      it.item_base = first;
+      it.pad = 0;
+      for (int j = 0; j < kInlinePages; ++j)
+        it.pages[j] = (it.page_begin + j < it.page_end) ? p.indices[it.page_begin + j] : -1;
+      p.items[first + sp] = it;
     }
     running += chunk_total;
+    __syncthreads();  // the next round rewrites scan and s_*
   }
   for (int i = t; i < p.batch * p.hkv; i += blockDim.x) p.counters[i] = 0;
   if (t == 0) {
