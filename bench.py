@@ -32,6 +32,10 @@ workload (same model, batch and mean context); otherwise null.
 ``cpu_baseline`` times the CPU oracle's gather-based attention on one layer of
 the same batch.
 
+``decode_attn_other_workloads`` times the same decode-attention kernel, the
+same way, on the Qwen2.5-7B (B=48, 28/4 heads) and Qwen2.5-72B (B=48, 64/8
+heads) decode shapes with their log-uniform contexts (synthetic pools).
+
 ``served`` reproduces the reference's published serving measurement
 (README.md:50-70, benchmark.py): the OpenAI-compatible server in a child
 process (random weights, synthetic tokenizer) and the streaming client at 2,
@@ -211,6 +215,45 @@ def served_leg(model: str, concurrency=(2, 20, 32), max_tokens: int = 50, runs: 
     return out
 
 
+def decode_attn_configs(dev) -> list:
+    """Decode attention alone on the other decode workloads' shapes: 32
+    synthetic layer pools (pages from a seeded permutation), one plan, the 32
+    launches captured in a graph and replayed between HIP events, as in the
+    roofline leg.  Contexts log-uniform as the workloads draw them."""
+    import torch
+
+    from minimal_inference_amd.decode import BatchDecodeWithPagedKVCacheWrapper
+
+    def loguniform(n, lo, hi, seed):
+        g = torch.Generator().manual_seed(seed)
+        x = torch.rand(n, generator=g, dtype=torch.float64) * (math.log(hi) - math.log(lo)) + math.log(lo)
+        return [int(round(math.exp(v))) for v in x.tolist()], g
+
+    out = []
+    for name, hq, hkv, d, (lens, g) in [("qwen2.5-7b B=48, contexts log-uniform [256, 4096] seed 3", 28, 4, 128,
+                                         loguniform(48, 256, 4096, 3)),
+                                        ("qwen2.5-72b B=48, contexts log-uniform [512, 4096] seed 4", 64, 8, 128,
+                                         loguniform(48, 512, 4096, 4))]:
+        B, L = len(lens), 32
+        npg = [math.ceil(n / 16) for n in lens]
+        tot = sum(npg)
+        perm = torch.randperm(tot + 1, generator=g)[:tot].to(torch.int32).to(dev)
+        pools = [torch.randn(tot + 1, 2, 16, hkv, d, device=dev, dtype=torch.bfloat16) for _ in range(L)]
+        ip = torch.tensor([0] + torch.tensor(npg).cumsum(0).tolist(), dtype=torch.int32, device=dev)
+        lp = torch.tensor([n - (p - 1) * 16 for n, p in zip(lens, npg)], dtype=torch.int32, device=dev)
+        qs = [torch.randn(B, hq, d, device=dev, dtype=torch.bfloat16) for _ in range(L)]
+        outs = [torch.empty_like(q) for q in qs]
+        w = BatchDecodeWithPagedKVCacheWrapper(torch.empty(128 << 20, dtype=torch.uint8, device=dev))
+        w.plan(ip, perm, lp, hq, hkv, d, 16)
+        us = time_us(lambda: [w.run(qs[l], pools[l], out=outs[l]) for l in range(L)], 1) / L
+        nbytes = sum(lens) * hkv * d * 4 + 2 * B * hq * d * 2 + 4 * ((B + 1) + tot + B)
+        gbps = nbytes / us / 1e3
+        out.append({"workload": name, "us": round(us, 2), "mb": round(nbytes / 1e6, 1), "gbps": round(gbps, 1),
+                    "frac": round(gbps / PEAK_HBM_GBPS, 4)})
+        del pools, qs, outs
+    return out
+
+
 def measured_traffic(model: str, batch: int, mean_context: float):
     """HBM bytes per attention launch from the committed counter summary, or
     None when it was measured on another workload."""
@@ -359,6 +402,8 @@ def main() -> int:
 
     path = path_kernel_times(sch, cfg, reqs, lens, dev)
     log(f"path kernels: {path}")
+    other_attn = decode_attn_configs(dev)
+    log(f"decode attention, other workloads: {other_attn}")
 
     # ---------------- CPU baseline: the oracle on one layer of the same batch
     cpu = None
@@ -429,6 +474,7 @@ def main() -> int:
                      "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic},
         "cpu_baseline": cpu,
         "path_kernels": path,
+        "decode_attn_other_workloads": other_attn,
         "served": served,
     }
     print(json.dumps(line), flush=True)
