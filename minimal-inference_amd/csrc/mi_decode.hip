@@ -25,13 +25,18 @@
 //     operand, V comes from the gfx950 LDS transpose read.
 //
 // Split merge without cache flushes.  Units of a request with several splits
-// write (O, m, l) partials with device-coherent (sc1, write-through) stores,
+// write (O, m, l) partials -- O rows as bf16, m and l as fp32; the merged
+// output is bf16 anyway, and bf16 rows halve the partial traffic and let one
+// merge round trip cover twice as many splits -- with device-coherent
+// (sc1, write-through) stores,
 // wait for them, and bump a per-(request, KV head) counter; the unit that
 // sees the count reach nsplit-1 reads the partials back with device-coherent
 // loads, merges them, and resets the counter.  No agent-scope fence (and so
 // no whole-L2 writeback / invalidate) is executed, and run() is one launch
 // with no memset.
 #include <math.h>
+
+#include <type_traits>
 
 #include "mi_common.h"
 
@@ -105,7 +110,7 @@ DecodeLayout decode_layout(int batch, int hq, int hkv, int head_dim, int max_uni
   L.pml = off;
   off = mi::align_up(off + size_t(max_units) * group * 2 * sizeof(float), 256);
   L.po = off;
-  off = mi::align_up(off + size_t(max_units) * group * head_dim * sizeof(float), 256);
+  off = mi::align_up(off + size_t(max_units) * group * head_dim * sizeof(uint16_t), 256);
   L.total = off;
   return L;
 }
@@ -116,7 +121,7 @@ int units_that_fit(size_t bytes, int batch, int hq, int hkv, int head_dim) {
   const int group = hq / hkv;
   const size_t fixed = 256 + 2 * 256 + size_t(batch) * hkv * sizeof(int);
   if (bytes <= fixed) return 0;
-  const size_t per_unit = sizeof(DecodeItem) / size_t(hkv) + 1 + size_t(group) * (2 + head_dim) * sizeof(float);
+  const size_t per_unit = sizeof(DecodeItem) / size_t(hkv) + 1 + size_t(group) * (2 * sizeof(float) + head_dim * sizeof(uint16_t));
   size_t n = (bytes - fixed) / per_unit;
   n = n > 65536 ? 65536 : n;
   while (n > 0 && decode_layout(batch, hq, hkv, head_dim, int(n)).total > bytes) n -= hkv;
@@ -282,9 +287,13 @@ struct DecodeTraits {
   static constexpr int SLOT = 4 * kPageSize * RS;  // two pages of K and V in LDS
   // Pages in flight per wave (~128-160 registers of staging).
   static constexpr int NB = (D == 64) ? MI_DECODE_NB64 : (D == 128) ? MI_DECODE_NB128 : 2;
-  static constexpr int OUT = D / 64;  // merged outputs per head per lane
+  static constexpr int OUT = D / 64;  // merged outputs per head per lane (contiguous dims)
+  // A split's bf16 partial row of one head, for one lane: OUT dims in 2, 4
+  // or 8 bytes (one or two registers).
+  using Part = typename std::conditional<D == 64, uint16_t, typename std::conditional<D == 128, uint32_t, uint64_t>::type>::type;
+  static constexpr int PREGS = D == 256 ? 2 : 1;
   // Splits whose partial rows one merge batch loads together (<= 96 registers).
-  static constexpr int KB_RAW = MI_DECODE_KB_REGS / (G * OUT);
+  static constexpr int KB_RAW = MI_DECODE_KB_REGS / (G * PREGS);
   static constexpr int KB = KB_RAW > 16 ? 16 : (KB_RAW < 1 ? 1 : KB_RAW);
   static_assert(G >= 1 && G <= 16, "group size");
   static_assert((NB - 1) * 2 * LPI <= 63, "vmcnt range");
@@ -296,7 +305,7 @@ struct RunParams {
   const DecodeItem* items;
   int* counters;
   float* pml;
-  float* po;
+  uint16_t* po;  // bf16 partial O rows
   const uint16_t* q;
   int64_t q_sb, q_sh;
   const char* pool;
@@ -621,13 +630,13 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
 
   // ---- split-K: publish the partial (write-through), count, last unit merges
   {
-    float* po = p.po + int64_t(u) * G * D;
+    uint16_t* po = p.po + int64_t(u) * G * D;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int h = 4 * g + i;
       if (h < G) {
 #pragma unroll
-        for (int t = 0; t < T::NT; ++t) partial_store<XL>(po + h * D + 16 * t + j, acc[t][i]);
+        for (int t = 0; t < T::NT; ++t) partial_store<XL>(po + h * D + 16 * t + j, mi::f32_to_bf16(acc[t][i]));
       }
     }
     if (lane < G) {  // lane h holds m_run / lt of head h
@@ -658,15 +667,14 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
 #pragma unroll
     for (int k = 0; k < T::OUT; ++k) sum[h][k] = 0.f;
   }
-  auto load_rows = [&](float (&v)[T::KB][G][T::OUT], int r0, int s0, int nr) {
+  using Part = typename T::Part;
+  auto load_rows = [&](Part (&v)[T::KB][G], int r0, int s0, int nr) {
 #pragma unroll
     for (int q = 0; q < T::KB; ++q) {
       const int s = r0 + min(s0 + q, nr - 1);
-      const float* src = p.po + int64_t((item_base + s) * p.hkv + hkv) * G * D;
+      const uint16_t* src = p.po + int64_t((item_base + s) * p.hkv + hkv) * G * D;
 #pragma unroll
-      for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int k = 0; k < T::OUT; ++k) v[q][h][k] = partial_load<XL>(src + h * D + lane + 64 * k);
+      for (int h = 0; h < G; ++h) v[q][h] = partial_load<XL>(reinterpret_cast<const Part*>(src + h * D) + lane);
     }
   };
   for (int r0 = 0; r0 < nsplit; r0 += 64) {
@@ -678,7 +686,7 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
       ms[h] = partial_load<XL>(p.pml + (int64_t(my_unit) * G + h) * 2 + 0);
       ls[h] = partial_load<XL>(p.pml + (int64_t(my_unit) * G + h) * 2 + 1);
     }
-    float v[T::KB][G][T::OUT];
+    Part v[T::KB][G];
     load_rows(v, r0, 0, nr);
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -701,7 +709,8 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
         for (int h = 0; h < G; ++h) {
           const float ws = mi::read_lane(wgt[h], s0 + q);
 #pragma unroll
-          for (int k = 0; k < T::OUT; ++k) sum[h][k] += ws * v[q][h][k];
+          for (int k = 0; k < T::OUT; ++k)
+            sum[h][k] += ws * mi::bf16_to_f32(uint16_t(uint64_t(v[q][h]) >> (16 * k)));
         }
       }
     }
@@ -711,7 +720,7 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
     const float inv = Lt[h] > 0.f ? 1.f / Lt[h] : 0.f;
     uint16_t* orow = p.out + int64_t(b) * p.o_sb + int64_t(hkv * G + h) * p.o_sh;
 #pragma unroll
-    for (int k = 0; k < T::OUT; ++k) orow[lane + 64 * k] = mi::f32_to_bf16(sum[h][k] * inv);
+    for (int k = 0; k < T::OUT; ++k) orow[lane * T::OUT + k] = mi::f32_to_bf16(sum[h][k] * inv);
   }
   if (lane == 0) coherent_store(counter, 0);
 }
@@ -842,7 +851,7 @@ extern "C" int mi_decode_run(void* workspace, size_t workspace_bytes, const void
   rp.items = reinterpret_cast<const DecodeItem*>(ws + L.items);
   rp.counters = reinterpret_cast<int*>(ws + L.counters);
   rp.pml = reinterpret_cast<float*>(ws + L.pml);
-  rp.po = reinterpret_cast<float*>(ws + L.po);
+  rp.po = reinterpret_cast<uint16_t*>(ws + L.po);
   rp.q = static_cast<const uint16_t*>(q);
   rp.q_sb = q_stride_batch;
   rp.q_sh = q_stride_head;
