@@ -60,6 +60,9 @@ constexpr int kUnitsPerCU = MI_DECODE_UNITS_PER_CU;
 #ifndef MI_DECODE_RS_PAD
 #define MI_DECODE_RS_PAD 16
 #endif
+#ifndef MI_DECODE_CLASS_SLACK
+#define MI_DECODE_CLASS_SLACK 8
+#endif
 #ifndef MI_DECODE_KB_REGS
 #define MI_DECODE_KB_REGS 96
 #endif
@@ -80,17 +83,19 @@ struct alignas(128) DecodeItem {
   int split;
   int nsplit;
   int item_base;  // item index of split 0 of this request
-  int pad;
+  int stride;     // item index step between consecutive splits of the request
 };
 static_assert(sizeof(DecodeItem) == 128, "item is read as 32 lanes x 4 bytes");
 constexpr int kItemB = kInlinePages, kItemBegin = kInlinePages + 1, kItemEnd = kInlinePages + 2,
-              kItemLast = kInlinePages + 3, kItemNsplit = kInlinePages + 5, kItemBase = kInlinePages + 6;
+              kItemLast = kInlinePages + 3, kItemNsplit = kInlinePages + 5, kItemBase = kInlinePages + 6,
+              kItemStride = kInlinePages + 7;
 
 struct DecodeHeader {
   int num_units;
   int num_items;
   int chunk_pages;
   int error;
+  int xl;  // 1: every unit of a (request, KV head) runs on one XCD
 };
 
 struct DecodeLayout {
@@ -136,10 +141,16 @@ struct PlanParams {
   const int32_t* indices;
   const int32_t* last_page_len;
   int batch, hkv, target_units, max_items;
+  // Items are laid out in `rep` interleaved classes (item i in class i % rep;
+  // every item of a request in one class) so that all units of one (request,
+  // KV head) run on one XCD; xl_flat: that already holds with rep = 1.
+  int rep, xl_flat;
   DecodeHeader* header;
   DecodeItem* items;
   int* counters;
 };
+
+constexpr int kMaxRep = 8;
 
 __device__ int block_sum(int v, int* scratch) {
   // Wave sums by xor-shuffle, then the per-wave partials through LDS.
@@ -166,32 +177,81 @@ __device__ int block_max(int v, int* scratch) {
   return s;
 }
 
-// Inclusive scan over the block (Hillis-Steele in LDS); *total receives the
-// block-wide sum.  Ends with a barrier, so `buf` may be reused at once.
-__device__ int block_inclusive_scan(int v, int* buf, int* total) {
-  const int t = threadIdx.x;
-  buf[t] = v;
-  __syncthreads();
-  for (int o = 1; o < int(blockDim.x); o <<= 1) {
-    int add = (t >= o) ? buf[t - o] : 0;
-    __syncthreads();
-    buf[t] += add;
-    __syncthreads();
+// Inclusive scan over the block: shuffles inside each wave, then the wave
+// totals through LDS (two barriers).  *total receives the block-wide sum.
+__device__ int block_scan(int v, int* wsum, int* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = int(blockDim.x >> 6);
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(v, o);
+    if (lane >= o) v += y;
   }
-  const int r = buf[t];
-  *total = buf[blockDim.x - 1];
+  __syncthreads();  // the previous call's readers are done with wsum
+  if (lane == 63) wsum[w] = v;
   __syncthreads();
-  return r;
+  int pre = 0, tot = 0;
+  for (int i = 0; i < nw; ++i) {
+    const int s = wsum[i];
+    pre += (i < w) ? s : 0;
+    tot += s;
+  }
+  *total = tot;
+  return v + pre;
+}
+
+__device__ __forceinline__ int request_pages(const PlanParams& p, int b) {
+  return max(0, p.indptr[b + 1] - p.indptr[b]);
+}
+__device__ __forceinline__ int items_of(int np, int chunk) { return max(1, (np + chunk - 1) / chunk); }
+// Class of a request whose items occupy [first, first + n) of all T items in
+// request order: the class whose share of that range holds the request's
+// midpoint, so classes take contiguous runs of requests of about T / rep
+// items each.
+__device__ __forceinline__ int class_of(int first, int n, int T, int rep) {
+  return min(rep - 1, int((2LL * first + n) * rep / (2LL * T)));
+}
+
+// Items (padding included) of the layout for `chunk` pages per item; with
+// rep > 1 also leaves each class's item count in cnt[] and its first item
+// (in request order) in start[].
+__device__ int layout_items(const PlanParams& p, int chunk, int rep, int* red, int* cnt, int* start) {
+  const int t = threadIdx.x;
+  int tot = 0;
+  for (int b = t; b < p.batch; b += blockDim.x) tot += items_of(request_pages(p, b), chunk);
+  const int T = block_sum(tot, red);
+  if (rep == 1) return T;
+  if (t < kMaxRep) {
+    cnt[t] = 0;
+    start[t] = T;
+  }
+  int running = 0;
+  for (int base = 0; base < p.batch; base += blockDim.x) {
+    const int b = base + t;
+    const int n = b < p.batch ? items_of(request_pages(p, b), chunk) : 0;
+    int round_total;
+    const int incl = block_scan(n, red, &round_total);  // its barriers also order the cnt / start resets
+    if (b < p.batch) {
+      const int first = running + incl - n;
+      const int c = class_of(first, n, T, rep);
+      atomicAdd(&cnt[c], n);
+      atomicMin(&start[c], first);
+    }
+    running += round_total;
+  }
+  __syncthreads();
+  int mx = 0;
+  for (int c = 0; c < rep; ++c) mx = max(mx, cnt[c]);
+  return rep * mx;
 }
 
 __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
   __shared__ int red[16];
   __shared__ int scan[1024];
   __shared__ int s_np[1024], s_pb0[1024], s_lpl[1024];
+  __shared__ int cnt[kMaxRep], start[kMaxRep];
   const int t = threadIdx.x;
   int mx = 0, tot = 0;
   for (int b = t; b < p.batch; b += blockDim.x) {
-    const int np = max(0, p.indptr[b + 1] - p.indptr[b]);
+    const int np = request_pages(p, b);
     mx = max(mx, np);
     tot += np;
   }
@@ -205,24 +265,43 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
   const int round_items = max(1, p.target_units / p.hkv);
   int limit = ((p.batch + round_items - 1) / round_items) * round_items;
   limit = min(max(limit, 1), p.max_items);
+  int hi = max(max_np, 1);
   // every chunk below total / limit has more than `limit` items (each
   // request has at least ceil(np / chunk) of them)
-  int hi = max(max_np, 1);
   int lo = min(hi, max(1, int((total_np + limit - 1) / limit)));
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
-    int cnt = 0;
-    for (int b = t; b < p.batch; b += blockDim.x) {
-      const int np = max(0, p.indptr[b + 1] - p.indptr[b]);
-      cnt += max(1, (np + mid - 1) / mid);
-    }
-    if (block_sum(cnt, red) <= limit) hi = mid; else lo = mid + 1;
+    if (layout_items(p, mid, 1, red, cnt, start) <= limit) hi = mid; else lo = mid + 1;
   }
-  const int chunk = lo;
+  int chunk = lo;
+  // The class layout pads every class to the largest, which can force
+  // longer items; it is taken when its items are at most 1/8 longer
+  // (MI_DECODE_CLASS_SLACK), else items are laid out in request order.
+  int rep = p.rep;
+  if (rep > 1) {
+    int hi2 = chunk + chunk / MI_DECODE_CLASS_SLACK;
+    if (layout_items(p, hi2, rep, red, cnt, start) > limit) {
+      rep = 1;
+    } else {
+      int lo2 = chunk;
+      while (lo2 < hi2) {
+        const int mid = (lo2 + hi2) >> 1;
+        if (layout_items(p, mid, rep, red, cnt, start) <= limit) hi2 = mid; else lo2 = mid + 1;
+      }
+      chunk = lo2;
+    }
+  }
+  const int num_items = layout_items(p, chunk, rep, red, cnt, start);  // leaves cnt / start for chunk
+  int T = num_items;
+  if (rep > 1) {
+    T = 0;
+    for (int c = 0; c < rep; ++c) T += cnt[c];
+  }
   // Items, 1024 requests at a time: the scan gives each request's first
   // item, then every thread writes whole items (one item per thread per
   // round, its inline page ids loaded together), finding the item's request
-  // by binary search over the scan.
+  // by binary search over the scan.  Request order position k of a request
+  // in class c goes to item (k - start[c]) * rep + c.
   int running = 0;
   for (int base = 0; base < p.batch; base += blockDim.x) {
     const int b = base + t;
@@ -230,14 +309,15 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
     if (b < p.batch) {
       pb0 = p.indptr[b];
       np = max(0, p.indptr[b + 1] - pb0);
-      ns = max(1, (np + chunk - 1) / chunk);
+      ns = items_of(np, chunk);
       lpl = min(max(p.last_page_len[b], 1), kPageSize);
     }
     s_np[t] = np;
     s_pb0[t] = pb0;
     s_lpl[t] = lpl;
     int chunk_total = 0;
-    block_inclusive_scan(ns, scan, &chunk_total);  // its barriers also publish s_np / s_pb0 / s_lpl
+    scan[t] = block_scan(ns, red, &chunk_total);
+    __syncthreads();  // publishes scan and s_np / s_pb0 / s_lpl
     for (int idx = t; idx < chunk_total; idx += blockDim.x) {
       int lo_r = 0, hi_r = int(blockDim.x) - 1;  // request r: the first with scan[r] > idx
       while (lo_r < hi_r) {
@@ -247,7 +327,13 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
       const int r = lo_r;
       const int nsr = scan[r] - (r > 0 ? scan[r - 1] : 0);
       const int first = running + scan[r] - nsr;
-      if (first + nsr > p.max_items) continue;  // the request does not fit: none of its items
+      int item_base = first, stride = 1;
+      if (rep > 1) {
+        const int c = class_of(first, nsr, T, rep);
+        item_base = (first - start[c]) * rep + c;
+        stride = rep;
+      }
+      if (item_base + (nsr - 1) * stride >= p.max_items) continue;  // the request does not fit: none of its items
       const int sp = idx - (scan[r] - nsr);
       const int npr = s_np[r];
       DecodeItem it;
@@ -257,22 +343,39 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
       it.last_valid = (npr == 0) ? 0 : (sp == nsr - 1 ? s_lpl[r] : kPageSize);
       it.split = sp;
       it.nsplit = nsr;
-      it.item_base = first;
-      it.pad = 0;
+      it.item_base = item_base;
+      it.stride = stride;
       for (int j = 0; j < kInlinePages; ++j)
         it.pages[j] = (it.page_begin + j < it.page_end) ? p.indices[it.page_begin + j] : -1;
-      p.items[first + sp] = it;
+      p.items[item_base + sp * stride] = it;
     }
     running += chunk_total;
     __syncthreads();  // the next round rewrites scan and s_*
   }
+  // padding items of the shorter classes: no pages, nsplit 0 (skipped)
+  if (rep > 1) {
+    for (int idx = t; idx < num_items; idx += blockDim.x) {
+      if (idx / rep < cnt[idx % rep]) continue;
+      DecodeItem it;
+      for (int j = 0; j < kInlinePages; ++j) it.pages[j] = -1;
+      it.b = 0;
+      it.page_begin = it.page_end = 0;
+      it.last_valid = 0;
+      it.split = 0;
+      it.nsplit = 0;
+      it.item_base = idx;
+      it.stride = rep;
+      p.items[idx] = it;
+    }
+  }
   for (int i = t; i < p.batch * p.hkv; i += blockDim.x) p.counters[i] = 0;
   if (t == 0) {
-    const int items = min(running, p.max_items);
+    const int items = min(num_items, p.max_items);
     p.header->num_items = items;
     p.header->num_units = items * p.hkv;
     p.header->chunk_pages = chunk;
-    p.header->error = (running > p.max_items) ? 1 : 0;
+    p.header->error = (num_items > p.max_items) ? 1 : 0;
+    p.header->xl = (rep > 1) ? 1 : p.xl_flat;
   }
 }
 
@@ -418,8 +521,8 @@ __device__ __forceinline__ int load_item_word(const RunParams& p, int u) {
 //                accumulator each lane already holds, and V comes from the
 //                LDS transpose read (lane (g, j) gets V[4g..4g+3][16t + j]);
 //                O[head 4g+i][16t + j] accumulates in registers.
-template <int D, int G, bool XL>
-__device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, lds_t* lds) {
+template <int D, int G, int W, bool XL>
+__device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, lds_t* wg_lds) {
   using T = DecodeTraits<D, G>;
   using Regs = PageRegs<D, G>;
   const int lane = threadIdx.x & 63;
@@ -430,6 +533,8 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
   const int last_valid = mi::read_lane_i(iv, kItemLast);
   const int nsplit = mi::read_lane_i(iv, kItemNsplit);
   const int item_base = mi::read_lane_i(iv, kItemBase);
+  const int stride = mi::read_lane_i(iv, kItemStride);
+  if (nsplit == 0) return;  // a padding item (the same for every wave of the workgroup)
   const int g = lane >> 4, j = lane & 15;
 
   // Q^T as the B operand: column j = head j of the group (zero when j >= G:
@@ -446,16 +551,24 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
       qb[s] = __builtin_bit_cast(mi::bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(rq, qoff, s * 64, 0));
   }
 
-  // Byte offsets inside a page: lane part (voffset) and instruction part
-  // (soffset).  Load i covers token rows (lane & 7) + 8 * (i & 1) and 16-byte
-  // chunk (lane >> 3) + 8 * (i >> 1): 128 contiguous bytes per row, which
-  // streams measurably faster than the 64 bytes per row an MFMA operand
-  // layout would allow.
+  // The W waves of a workgroup run heads h0 .. h0 + W - 1 of one item and
+  // load its pages together: wave w loads token rows [w RPW, (w + 1) RPW) of
+  // all W heads -- W * D * 2 contiguous bytes per row, which streams
+  // measurably faster than one head's D * 2 -- and every lane stages its 16
+  // bytes into the LDS slot of the head they belong to.  Byte offsets inside
+  // a page: lane part (voffset), instruction part (soffset).
+  constexpr int SW = W * D * 2, LPR = SW / 16, RPI = 64 / LPR, RPW = kPageSize / W;
+  static_assert(SW <= 1024 && RPW == RPI * T::LPI, "load layout");
   const int tok_bytes = p.hkv * D * 2;
   const int kv_bytes = kPageSize * tok_bytes;
   const int page_bytes = 2 * kv_bytes;
-  const int lrow = lane & 7, lchunk = lane >> 3;
-  const int voff = lrow * tok_bytes + hkv * D * 2 + lchunk * 16;
+  const int w = (W == 1) ? 0 : __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const int row0 = w * RPW;
+  const int lrow = lane / LPR, lbyte = (lane % LPR) * 16;
+  const int lhead = lbyte / (D * 2), lchunk = (lbyte % (D * 2)) / 16;
+  const int voff = lrow * tok_bytes + (hkv - w) * D * 2 + lbyte;
+  lds_t* const lds = wg_lds + w * T::SLOT;  // this wave's head
+  lds_t* const stage_lds = wg_lds + lhead * T::SLOT;  // the head of this lane's loaded bytes
 
   int pidv = iv;  // page ids of the current group, lane k = page k of the group
 
@@ -469,7 +582,7 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
         __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, ok ? page_bytes : 0, kBufferWord3);
 #pragma unroll
     for (int i = 0; i < T::LPI; ++i) {
-      const int so = 8 * (i & 1) * tok_bytes + 128 * (i >> 1);
+      const int so = (row0 + i * RPI) * tok_bytes;
       r.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, so, 0);
       r.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, so + kv_bytes, 0);
     }
@@ -490,24 +603,27 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
   // (g, j) holds tokens 4g+i of both pages) and whose B operand is the two
   // pages' transpose reads in the same token order.
   auto stage = [&](const Regs& r, int valid, int which) {
-    // the page to LDS (V rows past `valid` as zeros on a partial page: P is
-    // 0 there, but 0 * NaN would poison the MFMA)
-    lds_t* kl = k_slot(which);
-    lds_t* vl = v_slot(which);
+    // this wave's rows of the page to LDS (V rows past `valid` as zeros on a
+    // partial page: P is 0 there, but 0 * NaN would poison the MFMA)
+    lds_t* kl = stage_lds + which * 2 * kPageSize * T::RS + lrow * T::RS + lchunk * 16;
+    lds_t* vl = kl + kPageSize * T::RS;
 #pragma unroll
-    for (int i = 0; i < T::LPI; ++i)
-      lds_store16(kl + (lrow + 8 * (i & 1)) * T::RS + (lchunk + 8 * (i >> 1)) * 16, r.k[i]);
+    for (int i = 0; i < T::LPI; ++i) lds_store16(kl + (row0 + i * RPI) * T::RS, r.k[i]);
     if (valid == kPageSize) {
 #pragma unroll
-      for (int i = 0; i < T::LPI; ++i)
-        lds_store16(vl + (lrow + 8 * (i & 1)) * T::RS + (lchunk + 8 * (i >> 1)) * 16, r.v[i]);
+      for (int i = 0; i < T::LPI; ++i) lds_store16(vl + (row0 + i * RPI) * T::RS, r.v[i]);
     } else {
 #pragma unroll
       for (int i = 0; i < T::LPI; ++i) {
-        const int row = lrow + 8 * (i & 1);
-        lds_store16(vl + row * T::RS + (lchunk + 8 * (i >> 1)) * 16, (row < valid) ? r.v[i] : u32x4_t{0, 0, 0, 0});
+        const int row = row0 + i * RPI + lrow;
+        lds_store16(vl + (row0 + i * RPI) * T::RS, (row < valid) ? r.v[i] : u32x4_t{0, 0, 0, 0});
       }
     }
+  };
+  // the workgroup's waves exchange staged rows: LDS writes done, then a
+  // barrier (no wait on the page loads in flight)
+  auto wg_sync = [&]() {
+    if constexpr (W > 1) __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   };
   auto scores = [&](int which, int valid, float (&sv)[4]) {
     const lds_t* kl = k_slot(which);
@@ -522,6 +638,7 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
   auto consume2 = [&](const Regs& ra, int va, const Regs& rb, int vb) {
     stage(ra, va, 0);
     stage(rb, vb, 1);
+    wg_sync();
     float sa[4], sb[4];
     scores(0, va, sa);
     scores(1, vb, sb);
@@ -564,6 +681,7 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
       const mi::bf16x8_t vbop = __builtin_bit_cast(mi::bf16x8_t, (s16x8_t){x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]});
       acc[t] = mi::mfma_16x16x32_bf16(pa, vbop, acc[t]);
     }
+    wg_sync();  // every wave is done reading the slots before they are restaged
   };
 
   // ---- stream the pages: groups of page ids (the item's inline copy first,
@@ -672,14 +790,14 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
 #pragma unroll
     for (int q = 0; q < T::KB; ++q) {
       const int s = r0 + min(s0 + q, nr - 1);
-      const uint16_t* src = p.po + int64_t((item_base + s) * p.hkv + hkv) * G * D;
+      const uint16_t* src = p.po + int64_t((item_base + s * stride) * p.hkv + hkv) * G * D;
 #pragma unroll
       for (int h = 0; h < G; ++h) v[q][h] = partial_load<XL>(reinterpret_cast<const Part*>(src + h * D) + lane);
     }
   };
   for (int r0 = 0; r0 < nsplit; r0 += 64) {
     const int nr = min(64, nsplit - r0);
-    const int my_unit = (item_base + r0 + min(lane, nr - 1)) * p.hkv + hkv;
+    const int my_unit = (item_base + (r0 + min(lane, nr - 1)) * stride) * p.hkv + hkv;
     float ms[G], ls[G], wgt[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -725,50 +843,65 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
   if (lane == 0) coherent_store(counter, 0);
 }
 
+// A workgroup of W waves runs units blockIdx * W + w, w < W: W consecutive
+// KV heads of one item (W divides kv_heads, and the unit count is a multiple
+// of kv_heads, so the waves of a workgroup run the same number of units).
 // head_dim <= 128: registers capped at 256 per wave, so at least two waves
 // share a SIMD (8 units per CU).  head_dim 256 needs the full register file.
-template <int D, int G, bool XL>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(D <= 128 ? MI_DECODE_WAVES : 1))) void decode_run_kernel(
+template <int D, int G, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 128 ? MI_DECODE_WAVES : 1))) void decode_run_kernel(
     RunParams p) {
-  __shared__ __attribute__((aligned(16))) char slot[DecodeTraits<D, G>::SLOT];
+  __shared__ __attribute__((aligned(16))) char slot[W * DecodeTraits<D, G>::SLOT];
   lds_t* lds = (lds_t*)slot;
-  int u = blockIdx.x;
+  int u = int(blockIdx.x) * W + int(threadIdx.x >> 6);
   // The first item is read before the unit count is known (in bounds either
-  // way), so the two reads are in flight together.
+  // way), so the reads are in flight together.
   int iv = load_item_word(p, u);
   const int num_units = p.header->num_units;
+  // plan() decides where split partials live: L2-local when every unit of a
+  // (request, KV head) runs on one XCD
+  const bool xl = p.header->xl != 0;
   while (u < num_units) {
-    decode_unit<D, G, XL>(p, u, iv, lds);
-    u += gridDim.x;
+    if (xl) decode_unit<D, G, W, true>(p, u, iv, lds);
+    else decode_unit<D, G, W, false>(p, u, iv, lds);
+    u += int(gridDim.x) * W;
     if (u < num_units) iv = load_item_word(p, u);
   }
 }
 
 typedef void (*RunKernel)(RunParams);
 
-template <int D, bool XL>
+template <int D, int W>
 RunKernel pick_group(int g) {
   switch (g) {
-    case 1: return decode_run_kernel<D, 1, XL>;
-    case 2: return decode_run_kernel<D, 2, XL>;
-    case 3: return decode_run_kernel<D, 3, XL>;
-    case 4: return decode_run_kernel<D, 4, XL>;
-    case 5: return decode_run_kernel<D, 5, XL>;
-    case 6: return decode_run_kernel<D, 6, XL>;
-    case 7: return decode_run_kernel<D, 7, XL>;
-    case 8: return decode_run_kernel<D, 8, XL>;
+    case 1: return decode_run_kernel<D, 1, W>;
+    case 2: return decode_run_kernel<D, 2, W>;
+    case 3: return decode_run_kernel<D, 3, W>;
+    case 4: return decode_run_kernel<D, 4, W>;
+    case 5: return decode_run_kernel<D, 5, W>;
+    case 6: return decode_run_kernel<D, 6, W>;
+    case 7: return decode_run_kernel<D, 7, W>;
+    case 8: return decode_run_kernel<D, 8, W>;
     default: return nullptr;
   }
 }
 
-RunKernel pick_kernel(int head_dim, int group, bool xl = false) {
+// KV heads per workgroup: two when kv_heads is even and a row slice of one
+// head is short (head_dim <= 128), else one.
+int waves_per_group(int head_dim, int hkv) { return (head_dim <= 128 && hkv % 2 == 0) ? 2 : 1; }
+
+RunKernel pick_kernel(int head_dim, int group, int waves) {
   switch (head_dim) {
-    case 64: return xl ? pick_group<64, true>(group) : pick_group<64, false>(group);
-    case 128: return xl ? pick_group<128, true>(group) : pick_group<128, false>(group);
-    case 256: return xl ? pick_group<256, true>(group) : pick_group<256, false>(group);
+    case 64: return waves == 2 ? pick_group<64, 2>(group) : pick_group<64, 1>(group);
+    case 128: return waves == 2 ? pick_group<128, 2>(group) : pick_group<128, 1>(group);
+    case 256: return waves == 1 ? pick_group<256, 1>(group) : nullptr;
     default: return nullptr;
   }
 }
+
+// Workgroups of the run launch: one resident round of units (capped by the
+// workspace), W units each.  plan() and run() both use it.
+int run_grid(int max_units, int waves) { return max(1, min(max_units, mi::num_cus() * kUnitsPerCU) / waves); }
 
 int check_shape(const char* who, int batch, int hq, int hkv, int head_dim, int page_size) {
   if (batch < 0 || hq <= 0 || hkv <= 0)
@@ -777,7 +910,7 @@ int check_shape(const char* who, int batch, int hq, int hkv, int head_dim, int p
     return mi::fail(MI_ERR_INVALID, "%s: num_qo_heads %d not a multiple of num_kv_heads %d", who, hq, hkv);
   if (page_size != kPageSize)
     return mi::fail(MI_ERR_UNSUPPORTED, "%s: page_size %d (built for 16)", who, page_size);
-  if (!pick_kernel(head_dim, hq / hkv))
+  if (!pick_kernel(head_dim, hq / hkv, waves_per_group(head_dim, hkv)))
     return mi::fail(MI_ERR_UNSUPPORTED, "%s: head_dim %d / group %d not built (head_dim 64/128/256, group 1..8)",
                     who, head_dim, hq / hkv);
   return MI_OK;
@@ -819,6 +952,19 @@ extern "C" int mi_decode_plan(void* workspace, size_t workspace_bytes, const int
   pp.hkv = num_kv_heads;
   pp.target_units = mi::num_cus() * kUnitsPerCU;
   pp.max_items = L.max_items;
+  // Item classes: workgroup x runs on XCD x mod nx; unit u = item * kv_heads
+  // + h runs on workgroup u / W.  With k = kv_heads / W workgroups per item,
+  // all units of a (request, h) share an XCD when nx divides k, or when k
+  // divides nx and the request's items are all congruent mod nx / k.
+  const int waves = waves_per_group(head_dim, num_kv_heads);
+  const int nx = mi::xcd_round_robin(static_cast<hipStream_t>(stream), false);
+  const int k = num_kv_heads / waves;
+  pp.rep = 1;
+  pp.xl_flat = 0;
+  if (nx > 0 && run_grid(max_units, waves) % nx == 0) {
+    if (k % nx == 0) pp.xl_flat = 1;
+    else if (nx % k == 0 && nx / k <= kMaxRep) pp.rep = nx / k;
+  }
   pp.header = reinterpret_cast<DecodeHeader*>(ws);
   pp.items = reinterpret_cast<DecodeItem*>(ws + L.items);
   pp.counters = reinterpret_cast<int*>(ws + L.counters);
@@ -865,14 +1011,8 @@ extern "C" int mi_decode_run(void* workspace, size_t workspace_bytes, const void
   rp.max_items = L.max_items;
   const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf(float(head_dim));
   rp.scale_log2 = scale * mi::kLog2e;
-  const int grid = min(max_units, mi::num_cus() * kUnitsPerCU);
-  // Units u = item * kv_heads + h run on workgroup u mod grid.  When
-  // workgroups go to XCDs round robin over n XCDs and n divides both
-  // kv_heads and the grid, every unit of one (request, KV head) lands on XCD
-  // h mod n, so the split partials can stay in that XCD's L2.
-  const int nx = mi::xcd_round_robin(static_cast<hipStream_t>(stream), false);
-  const bool xl = nx > 0 && num_kv_heads % nx == 0 && grid % nx == 0;
-  RunKernel k = pick_kernel(head_dim, num_qo_heads / num_kv_heads, xl);
-  hipLaunchKernelGGL(k, dim3(grid), dim3(64), 0, static_cast<hipStream_t>(stream), rp);
+  const int waves = waves_per_group(head_dim, num_kv_heads);
+  RunKernel k = pick_kernel(head_dim, num_qo_heads / num_kv_heads, waves);
+  hipLaunchKernelGGL(k, dim3(run_grid(max_units, waves)), dim3(64 * waves), 0, static_cast<hipStream_t>(stream), rp);
   return mi::check_launch("decode_run_kernel");
 }
