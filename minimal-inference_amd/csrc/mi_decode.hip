@@ -51,6 +51,12 @@ constexpr int kUnitsPerCU = MI_DECODE_UNITS_PER_CU;
 #ifndef MI_DECODE_NB128
 #define MI_DECODE_NB128 4
 #endif
+#ifndef MI_DECODE_NB128_SHORT
+#define MI_DECODE_NB128_SHORT 2
+#endif
+#ifndef MI_DECODE_SHORT_CHUNK
+#define MI_DECODE_SHORT_CHUNK 8
+#endif
 #ifndef MI_DECODE_NB64
 #define MI_DECODE_NB64 8
 #endif
@@ -62,6 +68,9 @@ constexpr int kUnitsPerCU = MI_DECODE_UNITS_PER_CU;
 #endif
 #ifndef MI_DECODE_CLASS_SLACK
 #define MI_DECODE_CLASS_SLACK 8
+#endif
+#ifndef MI_DECODE_MERGE_KB
+#define MI_DECODE_MERGE_KB 8
 #endif
 #ifndef MI_DECODE_KB_REGS
 #define MI_DECODE_KB_REGS 96
@@ -407,8 +416,9 @@ struct RunParams {
   const DecodeHeader* header;
   const DecodeItem* items;
   int* counters;
-  float* pml;
-  uint16_t* po;  // bf16 partial O rows
+  float* pml;    // per (unit, head): m, l
+  uint16_t* po;  // per (unit, head): bf16 partial O row
+  int pml_bytes, po_bytes;
   const uint16_t* q;
   int64_t q_sb, q_sh;
   const char* pool;
@@ -504,6 +514,200 @@ __device__ __forceinline__ int load_item_word(const RunParams& p, int u) {
   return reinterpret_cast<const int*>(p.items + idx)[threadIdx.x & 31];
 }
 
+// Max / sum over each aligned group of LR lanes (8, 16 or 32); every lane
+// gets the result.
+template <int LR>
+__device__ __forceinline__ float group_max(float x) {
+  static_assert(LR == 8 || LR == 16 || LR == 32, "group width");
+  x = fmaxf(x, mi::dpp<mi::kDppQuadSwap1>(x));
+  x = fmaxf(x, mi::dpp<mi::kDppQuadSwap2>(x));
+  x = fmaxf(x, mi::dpp<mi::kDppRowHalfMirror>(x));
+  if constexpr (LR >= 16) x = fmaxf(x, mi::dpp<mi::kDppRowMirror>(x));
+  if constexpr (LR >= 32) x = max_xor16(x);
+  return x;
+}
+template <int LR>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(LR == 8 || LR == 16 || LR == 32, "group width");
+  x += mi::dpp<mi::kDppQuadSwap1>(x);
+  x += mi::dpp<mi::kDppQuadSwap2>(x);
+  x += mi::dpp<mi::kDppRowHalfMirror>(x);
+  if constexpr (LR >= 16) x += mi::dpp<mi::kDppRowMirror>(x);
+  if constexpr (LR >= 32) x = sum_xor16(x);
+  return x;
+}
+
+// Split-K tail of a unit: publish the partial (O rows, m, l), count, and
+// the last unit of the (request, KV head) merges all splits.  XL: the
+// partials stay in the XCD's L2 (every split ran on this XCD), else they go
+// device-coherent (write-through, bypassing the L2 on the way back).
+//
+// Partial O rows are bf16 in "lane order": position j * NT + t of a head's
+// row holds dim 16 t + j, which is what lane (g, j) of the MFMA accumulators
+// holds for head 4 g + i, so a lane publishes a head with one contiguous
+// store of NT values.  The merge reads rows back 16 bytes per lane: one load
+// covers R = 1024 / (2 D) rows, lane l taking row l / LR (a head) and 16-byte
+// chunk l % LR; the splits' m and l are laid out the same way (lane l: head
+// l / LR of a row group, split l % LR of a split group), so the weight of
+// split s for a lane's head is a shuffle inside its LR-lane group.
+template <int D, int G, bool XL>
+__device__ __forceinline__ void publish_merge(const RunParams& p, int u, int b, int hkv, int nsplit, int item_base,
+                                              int stride, const mi::f32x4_t (&acc)[DecodeTraits<D, G>::NT],
+                                              float m_run, float lt) {
+  using T = DecodeTraits<D, G>;
+  constexpr int NT = T::NT;
+  constexpr int CP = XL ? 1 : 16;  // cache policy bits: sc0 (workgroup scope) / sc1 (device scope)
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, j = lane & 15;
+  const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(p.po, (short)0, p.po_bytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rml = __builtin_amdgcn_make_buffer_rsrc(p.pml, (short)0, p.pml_bytes, kBufferWord3);
+  {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * g + i;
+      if (h < G) {
+        uint32_t w[NT / 2];
+#pragma unroll
+        for (int t = 0; t < NT / 2; ++t) w[t] = mi::pack_bf16x2(acc[2 * t][i], acc[2 * t + 1][i]);
+        const int off = (u * G + h) * D * 2 + j * NT * 2;
+        if constexpr (NT == 4) {
+          __builtin_amdgcn_raw_buffer_store_b64((__attribute__((ext_vector_type(2))) unsigned int){w[0], w[1]}, rpo, off, 0, CP);
+        } else {
+#pragma unroll
+          for (int q = 0; q < NT / 8; ++q)
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]}, rpo,
+                                                   off + 16 * q, 0, CP);
+        }
+      }
+    }
+    if (lane < G)  // lane h holds m_run / lt of head h
+      __builtin_amdgcn_raw_buffer_store_b64(
+          (__attribute__((ext_vector_type(2))) unsigned int){__float_as_uint(m_run), __float_as_uint(lt)}, rml,
+          (u * G + lane) * 8, 0, CP);
+  }
+  // Wait until this wave's stores are acknowledged (vmcnt 0; expcnt /
+  // lgkmcnt left free), so they are visible before the counter moves.  The
+  // fence keeps the compiler from reordering around it.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  int prev = 0;
+  int* counter = p.counters + b * p.hkv + hkv;
+  if (lane == 0) prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  prev = mi::read_lane_i(prev, 0);
+  if (prev != nsplit - 1) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+
+  constexpr int R = 1024 / (2 * D);   // rows per 16-byte load: 4 (D 128), 8 (D 64), 2 (D 256)
+  constexpr int LR = 64 / R;          // lanes per row
+  constexpr int A = (G + R - 1) / R;  // row groups covering the G heads
+  constexpr int C = 64 / LR;          // split groups per round of 64 splits
+  constexpr int KB = MI_DECODE_MERGE_KB;  // splits whose rows are loaded together
+  static_assert(LR % KB == 0, "batches inside a split group");
+  const int hg = lane / LR, sg = lane % LR;
+  float M[A], Lt[A], sum[A][8];
+#pragma unroll
+  for (int a = 0; a < A; ++a) {
+    M[a] = -INFINITY;
+    Lt[a] = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) sum[a][k] = 0.f;
+  }
+  auto unit_of = [&](int s) { return (item_base + s * stride) * p.hkv + hkv; };
+  auto load_batch = [&](u32x4_t (&v)[KB][A], int s0, int nr) {
+#pragma unroll
+    for (int q = 0; q < KB; ++q) {
+      const int us = unit_of(min(s0 + q, nr - 1));
+#pragma unroll
+      for (int a = 0; a < A; ++a) {
+        const int h = min(a * R + hg, G - 1);
+        v[q][a] = __builtin_amdgcn_raw_buffer_load_b128(rpo, (us * G + h) * D * 2 + sg * 16, 0, CP);
+      }
+    }
+  };
+  for (int r0 = 0; r0 < nsplit; r0 += 64) {
+    const int nr = min(64, nsplit - r0);
+    // (m, l) of split c LR + sg, head a R + hg; the first rows load with them
+    typedef __attribute__((ext_vector_type(2))) unsigned int u32x2_t;
+    u32x2_t ml[A][C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int us = unit_of(r0 + min(c * LR + sg, nr - 1));
+#pragma unroll
+      for (int a = 0; a < A; ++a)
+        ml[a][c] = __builtin_amdgcn_raw_buffer_load_b64(rml, (us * G + min(a * R + hg, G - 1)) * 8, 0, CP);
+    }
+    u32x4_t v[KB][A];
+    load_batch(v, r0, r0 + nr);
+    float wgt[A][C];
+#pragma unroll
+    for (int a = 0; a < A; ++a) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int c = 0; c < C; ++c)
+        if (c * LR + sg < nr) mx = fmaxf(mx, __uint_as_float(ml[a][c].x));
+      const float Mn = fmaxf(M[a], group_max<LR>(mx));
+      const float f = (M[a] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M[a] - Mn);
+      Lt[a] *= f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) sum[a][k] *= f;
+      float ls = 0.f;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const float ms = __uint_as_float(ml[a][c].x);
+        wgt[a][c] = (c * LR + sg < nr && ms != -INFINITY) ? __builtin_amdgcn_exp2f(ms - Mn) : 0.f;
+        ls += wgt[a][c] * __uint_as_float(ml[a][c].y);
+      }
+      Lt[a] += group_sum<LR>(ls);
+      M[a] = Mn;
+    }
+#pragma nounroll
+    for (int c = 0; c < C; ++c) {
+      if (c * LR >= nr) break;
+      float wc[A];
+#pragma unroll
+      for (int a = 0; a < A; ++a) {
+        wc[a] = wgt[a][0];
+#pragma unroll
+        for (int cc = 1; cc < C; ++cc) wc[a] = (c == cc) ? wgt[a][cc] : wc[a];
+      }
+#pragma unroll
+      for (int q0 = 0; q0 < LR; q0 += KB) {
+        const int s0 = c * LR + q0;
+        if (s0 >= nr) break;
+        if (s0 > 0) load_batch(v, r0 + s0, r0 + nr);
+#pragma unroll
+        for (int q = 0; q < KB; ++q) {
+          if (s0 + q >= nr) break;
+#pragma unroll
+          for (int a = 0; a < A; ++a) {
+            const float w = mi::lane_shuffle(wc[a], hg * LR + q0 + q);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              sum[a][2 * k] += w * mi::bf16_lo(v[q][a][k]);
+              sum[a][2 * k + 1] += w * mi::bf16_hi(v[q][a][k]);
+            }
+          }
+        }
+      }
+    }
+  }
+  // lane (hg, sg) holds row positions 8 sg .. 8 sg + 7 of head a R + hg
+#pragma unroll
+  for (int a = 0; a < A; ++a) {
+    const int h = a * R + hg;
+    if (h < G) {
+      const float inv = Lt[a] > 0.f ? 1.f / Lt[a] : 0.f;
+      uint16_t* orow = p.out + int64_t(b) * p.o_sb + int64_t(hkv * G + h) * p.o_sh;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int pos = sg * 8 + k;
+        orow[16 * (pos % NT) + pos / NT] = mi::f32_to_bf16(sum[a][k] * inv);
+      }
+    }
+  }
+  if (lane == 0) coherent_store(counter, 0);
+}
+
 // One unit: (item, KV head).  Lane l of the wave is (g, j) = (l >> 4, l & 15).
 //
 //   page loads : raw buffer loads through a per-page descriptor (base = the
@@ -521,10 +725,11 @@ __device__ __forceinline__ int load_item_word(const RunParams& p, int u) {
 //                accumulator each lane already holds, and V comes from the
 //                LDS transpose read (lane (g, j) gets V[4g..4g+3][16t + j]);
 //                O[head 4g+i][16t + j] accumulates in registers.
-template <int D, int G, int W, bool XL>
-__device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, lds_t* wg_lds) {
+template <int D, int G, int W, int NB>
+__device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, lds_t* wg_lds, bool xl) {
   using T = DecodeTraits<D, G>;
   using Regs = PageRegs<D, G>;
+  static_assert((NB - 1) * 2 * T::LPI <= 63 && NB % 2 == 0, "vmcnt range; pages are consumed in pairs");
   const int lane = threadIdx.x & 63;
   const int hkv = u - (u / p.hkv) * p.hkv;
   const int b = mi::read_lane_i(iv, kItemB);
@@ -690,32 +895,32 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
   // descriptor -- and the only branches around code are VMEM-free (the tail
   // consumes), so the compiler's wait before consuming a page is exactly
   // "NB-1 pages still outstanding".
-  Regs buf[T::NB];
+  Regs buf[NB];
   int g_start = 0, gsize = min(npg, kInlinePages);
   while (true) {
 #pragma unroll
-    for (int s = 0; s < T::NB; ++s) issue(buf[s], s, gsize);
+    for (int s = 0; s < NB; ++s) issue(buf[s], s, gsize);
     auto page_valid = [&](int k) {
       const int valid = (g_start + k == npg - 1) ? last_valid : kPageSize;
       return page_ok(k, page_id(k), gsize) ? valid : 0;
     };
-    const int full = gsize / T::NB;
+    const int full = gsize / NB;
     for (int it = 0; it < full; ++it) {
 #pragma unroll
-      for (int s = 0; s < T::NB; s += 2) {
-        const int k = it * T::NB + s;
+      for (int s = 0; s < NB; s += 2) {
+        const int k = it * NB + s;
         consume2(buf[s], page_valid(k), buf[s + 1], page_valid(k + 1));
-        issue(buf[s], k + T::NB, gsize);
-        issue(buf[s + 1], k + 1 + T::NB, gsize);
+        issue(buf[s], k + NB, gsize);
+        issue(buf[s + 1], k + 1 + NB, gsize);
       }
     }
     // the last rem (< NB) pages; a pair's second page past the group's end
     // was loaded through a size-0 descriptor (zeros) and is fully masked
-    const int rem = gsize - full * T::NB;
+    const int rem = gsize - full * NB;
 #pragma unroll
-    for (int s = 0; s < T::NB - 1; s += 2)
-      if (s < rem) consume2(buf[s], page_valid(full * T::NB + s), buf[s + 1],
-                            s + 1 < rem ? page_valid(full * T::NB + s + 1) : 0);
+    for (int s = 0; s < NB - 1; s += 2)
+      if (s < rem) consume2(buf[s], page_valid(full * NB + s), buf[s + 1],
+                            s + 1 < rem ? page_valid(full * NB + s + 1) : 0);
     g_start += gsize;
     if (g_start >= npg) break;
     gsize = min(64, npg - g_start);
@@ -746,101 +951,8 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
     return;
   }
 
-  // ---- split-K: publish the partial (write-through), count, last unit merges
-  {
-    uint16_t* po = p.po + int64_t(u) * G * D;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * g + i;
-      if (h < G) {
-#pragma unroll
-        for (int t = 0; t < T::NT; ++t) partial_store<XL>(po + h * D + 16 * t + j, mi::f32_to_bf16(acc[t][i]));
-      }
-    }
-    if (lane < G) {  // lane h holds m_run / lt of head h
-      partial_store<XL>(p.pml + (int64_t(u) * G + lane) * 2 + 0, m_run);
-      partial_store<XL>(p.pml + (int64_t(u) * G + lane) * 2 + 1, lt);
-    }
-  }
-  // Wait until this wave's write-through stores are acknowledged (vmcnt 0;
-  // expcnt / lgkmcnt left free), so they are visible device-wide before the
-  // counter moves.  The fence keeps the compiler from reordering around it.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  int prev = 0;
-  int* counter = p.counters + b * p.hkv + hkv;
-  if (lane == 0) prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  prev = mi::read_lane_i(prev, 0);
-  if (prev != nsplit - 1) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-
-  // Online merge over the splits, 64 per round (lane s holds split s's m, l).
-  // The m / l loads and the first KB splits' partial rows are issued
-  // together, so a merge of up to KB splits costs one round trip.
-  float M[G], Lt[G], sum[G][T::OUT];
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    M[h] = -INFINITY;
-    Lt[h] = 0.f;
-#pragma unroll
-    for (int k = 0; k < T::OUT; ++k) sum[h][k] = 0.f;
-  }
-  using Part = typename T::Part;
-  auto load_rows = [&](Part (&v)[T::KB][G], int r0, int s0, int nr) {
-#pragma unroll
-    for (int q = 0; q < T::KB; ++q) {
-      const int s = r0 + min(s0 + q, nr - 1);
-      const uint16_t* src = p.po + int64_t((item_base + s * stride) * p.hkv + hkv) * G * D;
-#pragma unroll
-      for (int h = 0; h < G; ++h) v[q][h] = partial_load<XL>(reinterpret_cast<const Part*>(src + h * D) + lane);
-    }
-  };
-  for (int r0 = 0; r0 < nsplit; r0 += 64) {
-    const int nr = min(64, nsplit - r0);
-    const int my_unit = (item_base + (r0 + min(lane, nr - 1)) * stride) * p.hkv + hkv;
-    float ms[G], ls[G], wgt[G];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      ms[h] = partial_load<XL>(p.pml + (int64_t(my_unit) * G + h) * 2 + 0);
-      ls[h] = partial_load<XL>(p.pml + (int64_t(my_unit) * G + h) * 2 + 1);
-    }
-    Part v[T::KB][G];
-    load_rows(v, r0, 0, nr);
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      if (lane >= nr) ms[h] = -INFINITY;
-      const float Mn = fmaxf(M[h], wave_max_fast(ms[h]));
-      const float f = (M[h] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M[h] - Mn);
-      Lt[h] *= f;
-#pragma unroll
-      for (int k = 0; k < T::OUT; ++k) sum[h][k] *= f;
-      wgt[h] = (ms[h] != -INFINITY) ? __builtin_amdgcn_exp2f(ms[h] - Mn) : 0.f;
-      Lt[h] += wave_sum_fast(wgt[h] * ls[h]);
-      M[h] = Mn;
-    }
-    for (int s0 = 0; s0 < nr; s0 += T::KB) {
-      if (s0 > 0) load_rows(v, r0, s0, nr);
-#pragma unroll
-      for (int q = 0; q < T::KB; ++q) {
-        if (s0 + q >= nr) break;
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-          const float ws = mi::read_lane(wgt[h], s0 + q);
-#pragma unroll
-          for (int k = 0; k < T::OUT; ++k)
-            sum[h][k] += ws * mi::bf16_to_f32(uint16_t(uint64_t(v[q][h]) >> (16 * k)));
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const float inv = Lt[h] > 0.f ? 1.f / Lt[h] : 0.f;
-    uint16_t* orow = p.out + int64_t(b) * p.o_sb + int64_t(hkv * G + h) * p.o_sh;
-#pragma unroll
-    for (int k = 0; k < T::OUT; ++k) orow[lane * T::OUT + k] = mi::f32_to_bf16(sum[h][k] * inv);
-  }
-  if (lane == 0) coherent_store(counter, 0);
+  if (xl) publish_merge<D, G, true>(p, u, b, hkv, nsplit, item_base, stride, acc, m_run, lt);
+  else publish_merge<D, G, false>(p, u, b, hkv, nsplit, item_base, stride, acc, m_run, lt);
 }
 
 // A workgroup of W waves runs units blockIdx * W + w, w < W: W consecutive
@@ -861,9 +973,18 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 128
   // plan() decides where split partials live: L2-local when every unit of a
   // (request, KV head) runs on one XCD
   const bool xl = p.header->xl != 0;
+  // Short items (a few page pairs per unit) keep fewer pages in flight: the
+  // first pages of every wave arrive sooner, the rest overlaps across waves.
+  constexpr int NBL = DecodeTraits<D, G>::NB;
+  constexpr int NBS = (D == 128) ? MI_DECODE_NB128_SHORT : NBL;
+  const bool short_items = NBS != NBL && p.header->chunk_pages <= MI_DECODE_SHORT_CHUNK;
   while (u < num_units) {
-    if (xl) decode_unit<D, G, W, true>(p, u, iv, lds);
-    else decode_unit<D, G, W, false>(p, u, iv, lds);
+    if constexpr (NBS != NBL) {
+      if (short_items) decode_unit<D, G, W, NBS>(p, u, iv, lds, xl);
+      else decode_unit<D, G, W, NBL>(p, u, iv, lds, xl);
+    } else {
+      decode_unit<D, G, W, NBL>(p, u, iv, lds, xl);
+    }
     u += int(gridDim.x) * W;
     if (u < num_units) iv = load_item_word(p, u);
   }
@@ -998,6 +1119,8 @@ extern "C" int mi_decode_run(void* workspace, size_t workspace_bytes, const void
   rp.counters = reinterpret_cast<int*>(ws + L.counters);
   rp.pml = reinterpret_cast<float*>(ws + L.pml);
   rp.po = reinterpret_cast<uint16_t*>(ws + L.po);
+  rp.pml_bytes = int(L.po - L.pml);
+  rp.po_bytes = int(L.total - L.po);
   rp.q = static_cast<const uint16_t*>(q);
   rp.q_sb = q_stride_batch;
   rp.q_sh = q_stride_head;
