@@ -18,11 +18,6 @@ void clear_error();
 int check_launch(const char* what);
 // Number of compute units of the current device (cached per device).
 int num_cus();
-// n > 0 when workgroup i of a launch runs on XCD (i mod n) on the current
-// device, 0 when not (or not known).  With probe, the first call per device
-// runs a small kernel on `stream` and synchronises it (skipped, returning 0,
-// while the stream is capturing); without, only the cached answer is read.
-int xcd_round_robin(hipStream_t stream, bool probe);
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 

@@ -9,34 +9,34 @@
 // contiguous page ranges ("items") so that items x kv_heads ("units") fill
 // one resident round of kUnitsPerCU waves per CU, and copies the first
 // kInlinePages page ids of each item into the item, so a wave starts its page
-// loads right after reading the item.  One 64-lane wave runs one unit: it
-// streams the unit's K and V pages for one KV head and serves all `group` Q
-// heads of that KV head, so each KV byte is read from HBM once per step.
+// loads right after reading the item.  One 64-lane wave runs one unit and
+// serves all `group` Q heads of its KV head, so each KV byte is read from HBM
+// once per step; a workgroup of W waves (two for head_dim <= 128 and even
+// kv_heads) runs W neighbouring KV heads of one item and loads their pages
+// together, W * head_dim * 2 contiguous bytes per token row.
 //
 // Per 16-token page, one wave:
-//   * loads K and V through a per-page buffer descriptor (size 0 for an
-//     invalid or absent page: the loads return zeros and touch no memory),
-//     NB pages in flight, and stages them in LDS;
+//   * loads its share of the workgroup's K and V rows through a per-page
+//     buffer descriptor (size 0 for an invalid or absent page: the loads
+//     return zeros and touch no memory), NB pages in flight, and stages them
+//     in the LDS slot of the head they belong to (a barrier per page pair);
 //   * S^T = K Q^T with 16x16x32 bf16 MFMAs (Q columns are the group's heads,
 //     zero-padded to 16);
 //   * online softmax in the exp2 domain with a lazy running max (rescale only
 //     when the max grows by more than 2^8, so rescales are rare);
-//   * O += P V with 16x16x16 bf16 MFMAs: the S^T accumulator is already the P
-//     operand, V comes from the gfx950 LDS transpose read.
+//   * O += P V with 16x16x32 bf16 MFMAs over two pages: the S^T accumulators
+//     already are the P operand, V comes from the gfx950 LDS transpose read.
 //
 // Split merge without cache flushes.  Units of a request with several splits
-// write (O, m, l) partials -- O rows as bf16, m and l as fp32; the merged
-// output is bf16 anyway, and bf16 rows halve the partial traffic and let one
-// merge round trip cover twice as many splits -- with device-coherent
-// (sc1, write-through) stores,
-// wait for them, and bump a per-(request, KV head) counter; the unit that
-// sees the count reach nsplit-1 reads the partials back with device-coherent
-// loads, merges them, and resets the counter.  No agent-scope fence (and so
-// no whole-L2 writeback / invalidate) is executed, and run() is one launch
-// with no memset.
+// write (O, m, l) partials -- O rows as bf16 (the merged output is bf16
+// anyway; bf16 rows halve the partial traffic), m and l as fp32 -- with
+// device-coherent (sc1) 16-byte stores, wait for them, and bump a
+// per-(request, KV head) counter; the unit that sees the count reach
+// nsplit-1 reads the partials back (16 bytes per lane, eight splits per
+// round trip), merges them, and resets the counter.  No agent-scope fence
+// (and so no whole-L2 writeback / invalidate) is executed, and run() is one
+// launch with no memset.
 #include <math.h>
-
-#include <type_traits>
 
 #include "mi_common.h"
 
@@ -66,15 +66,6 @@ constexpr int kUnitsPerCU = MI_DECODE_UNITS_PER_CU;
 #ifndef MI_DECODE_RS_PAD
 #define MI_DECODE_RS_PAD 16
 #endif
-#ifndef MI_DECODE_CLASS_SLACK
-#define MI_DECODE_CLASS_SLACK 8
-#endif
-#ifndef MI_DECODE_MERGE_KB
-#define MI_DECODE_MERGE_KB 8
-#endif
-#ifndef MI_DECODE_KB_REGS
-#define MI_DECODE_KB_REGS 96
-#endif
 constexpr int kInlinePages = 24;
 // s_waitcnt immediate (gfx9 encoding): vmcnt = 0, expcnt = 7, lgkmcnt = 15.
 constexpr int kWaitVmcnt0 = 0x0F70;
@@ -92,19 +83,17 @@ struct alignas(128) DecodeItem {
   int split;
   int nsplit;
   int item_base;  // item index of split 0 of this request
-  int stride;     // item index step between consecutive splits of the request
+  int pad;
 };
 static_assert(sizeof(DecodeItem) == 128, "item is read as 32 lanes x 4 bytes");
 constexpr int kItemB = kInlinePages, kItemBegin = kInlinePages + 1, kItemEnd = kInlinePages + 2,
-              kItemLast = kInlinePages + 3, kItemNsplit = kInlinePages + 5, kItemBase = kInlinePages + 6,
-              kItemStride = kInlinePages + 7;
+              kItemLast = kInlinePages + 3, kItemNsplit = kInlinePages + 5, kItemBase = kInlinePages + 6;
 
 struct DecodeHeader {
   int num_units;
   int num_items;
   int chunk_pages;
   int error;
-  int xl;  // 1: every unit of a (request, KV head) runs on one XCD
 };
 
 struct DecodeLayout {
@@ -150,16 +139,10 @@ struct PlanParams {
   const int32_t* indices;
   const int32_t* last_page_len;
   int batch, hkv, target_units, max_items;
-  // Items are laid out in `rep` interleaved classes (item i in class i % rep;
-  // every item of a request in one class) so that all units of one (request,
-  // KV head) run on one XCD; xl_flat: that already holds with rep = 1.
-  int rep, xl_flat;
   DecodeHeader* header;
   DecodeItem* items;
   int* counters;
 };
-
-constexpr int kMaxRep = 8;
 
 __device__ int block_sum(int v, int* scratch) {
   // Wave sums by xor-shuffle, then the per-wave partials through LDS.
@@ -211,52 +194,11 @@ __device__ __forceinline__ int request_pages(const PlanParams& p, int b) {
   return max(0, p.indptr[b + 1] - p.indptr[b]);
 }
 __device__ __forceinline__ int items_of(int np, int chunk) { return max(1, (np + chunk - 1) / chunk); }
-// Class of a request whose items occupy [first, first + n) of all T items in
-// request order: the class whose share of that range holds the request's
-// midpoint, so classes take contiguous runs of requests of about T / rep
-// items each.
-__device__ __forceinline__ int class_of(int first, int n, int T, int rep) {
-  return min(rep - 1, int((2LL * first + n) * rep / (2LL * T)));
-}
-
-// Items (padding included) of the layout for `chunk` pages per item; with
-// rep > 1 also leaves each class's item count in cnt[] and its first item
-// (in request order) in start[].
-__device__ int layout_items(const PlanParams& p, int chunk, int rep, int* red, int* cnt, int* start) {
-  const int t = threadIdx.x;
-  int tot = 0;
-  for (int b = t; b < p.batch; b += blockDim.x) tot += items_of(request_pages(p, b), chunk);
-  const int T = block_sum(tot, red);
-  if (rep == 1) return T;
-  if (t < kMaxRep) {
-    cnt[t] = 0;
-    start[t] = T;
-  }
-  int running = 0;
-  for (int base = 0; base < p.batch; base += blockDim.x) {
-    const int b = base + t;
-    const int n = b < p.batch ? items_of(request_pages(p, b), chunk) : 0;
-    int round_total;
-    const int incl = block_scan(n, red, &round_total);  // its barriers also order the cnt / start resets
-    if (b < p.batch) {
-      const int first = running + incl - n;
-      const int c = class_of(first, n, T, rep);
-      atomicAdd(&cnt[c], n);
-      atomicMin(&start[c], first);
-    }
-    running += round_total;
-  }
-  __syncthreads();
-  int mx = 0;
-  for (int c = 0; c < rep; ++c) mx = max(mx, cnt[c]);
-  return rep * mx;
-}
 
 __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
   __shared__ int red[16];
   __shared__ int scan[1024];
   __shared__ int s_np[1024], s_pb0[1024], s_lpl[1024];
-  __shared__ int cnt[kMaxRep], start[kMaxRep];
   const int t = threadIdx.x;
   int mx = 0, tot = 0;
   for (int b = t; b < p.batch; b += blockDim.x) {
@@ -274,43 +216,21 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
   const int round_items = max(1, p.target_units / p.hkv);
   int limit = ((p.batch + round_items - 1) / round_items) * round_items;
   limit = min(max(limit, 1), p.max_items);
-  int hi = max(max_np, 1);
   // every chunk below total / limit has more than `limit` items (each
   // request has at least ceil(np / chunk) of them)
+  int hi = max(max_np, 1);
   int lo = min(hi, max(1, int((total_np + limit - 1) / limit)));
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
-    if (layout_items(p, mid, 1, red, cnt, start) <= limit) hi = mid; else lo = mid + 1;
+    int cnt = 0;
+    for (int b = t; b < p.batch; b += blockDim.x) cnt += items_of(request_pages(p, b), mid);
+    if (block_sum(cnt, red) <= limit) hi = mid; else lo = mid + 1;
   }
-  int chunk = lo;
-  // The class layout pads every class to the largest, which can force
-  // longer items; it is taken when its items are at most 1/8 longer
-  // (MI_DECODE_CLASS_SLACK), else items are laid out in request order.
-  int rep = p.rep;
-  if (rep > 1) {
-    int hi2 = chunk + chunk / MI_DECODE_CLASS_SLACK;
-    if (layout_items(p, hi2, rep, red, cnt, start) > limit) {
-      rep = 1;
-    } else {
-      int lo2 = chunk;
-      while (lo2 < hi2) {
-        const int mid = (lo2 + hi2) >> 1;
-        if (layout_items(p, mid, rep, red, cnt, start) <= limit) hi2 = mid; else lo2 = mid + 1;
-      }
-      chunk = lo2;
-    }
-  }
-  const int num_items = layout_items(p, chunk, rep, red, cnt, start);  // leaves cnt / start for chunk
-  int T = num_items;
-  if (rep > 1) {
-    T = 0;
-    for (int c = 0; c < rep; ++c) T += cnt[c];
-  }
+  const int chunk = lo;
   // Items, 1024 requests at a time: the scan gives each request's first
   // item, then every thread writes whole items (one item per thread per
   // round, its inline page ids loaded together), finding the item's request
-  // by binary search over the scan.  Request order position k of a request
-  // in class c goes to item (k - start[c]) * rep + c.
+  // by binary search over the scan.
   int running = 0;
   for (int base = 0; base < p.batch; base += blockDim.x) {
     const int b = base + t;
@@ -336,13 +256,7 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
       const int r = lo_r;
       const int nsr = scan[r] - (r > 0 ? scan[r - 1] : 0);
       const int first = running + scan[r] - nsr;
-      int item_base = first, stride = 1;
-      if (rep > 1) {
-        const int c = class_of(first, nsr, T, rep);
-        item_base = (first - start[c]) * rep + c;
-        stride = rep;
-      }
-      if (item_base + (nsr - 1) * stride >= p.max_items) continue;  // the request does not fit: none of its items
+      if (first + nsr > p.max_items) continue;  // the request does not fit: none of its items
       const int sp = idx - (scan[r] - nsr);
       const int npr = s_np[r];
       DecodeItem it;
@@ -352,39 +266,22 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
       it.last_valid = (npr == 0) ? 0 : (sp == nsr - 1 ? s_lpl[r] : kPageSize);
       it.split = sp;
       it.nsplit = nsr;
-      it.item_base = item_base;
-      it.stride = stride;
+      it.item_base = first;
+      it.pad = 0;
       for (int j = 0; j < kInlinePages; ++j)
         it.pages[j] = (it.page_begin + j < it.page_end) ? p.indices[it.page_begin + j] : -1;
-      p.items[item_base + sp * stride] = it;
+      p.items[first + sp] = it;
     }
     running += chunk_total;
     __syncthreads();  // the next round rewrites scan and s_*
   }
-  // padding items of the shorter classes: no pages, nsplit 0 (skipped)
-  if (rep > 1) {
-    for (int idx = t; idx < num_items; idx += blockDim.x) {
-      if (idx / rep < cnt[idx % rep]) continue;
-      DecodeItem it;
-      for (int j = 0; j < kInlinePages; ++j) it.pages[j] = -1;
-      it.b = 0;
-      it.page_begin = it.page_end = 0;
-      it.last_valid = 0;
-      it.split = 0;
-      it.nsplit = 0;
-      it.item_base = idx;
-      it.stride = rep;
-      p.items[idx] = it;
-    }
-  }
   for (int i = t; i < p.batch * p.hkv; i += blockDim.x) p.counters[i] = 0;
   if (t == 0) {
-    const int items = min(num_items, p.max_items);
+    const int items = min(running, p.max_items);
     p.header->num_items = items;
     p.header->num_units = items * p.hkv;
     p.header->chunk_pages = chunk;
-    p.header->error = (num_items > p.max_items) ? 1 : 0;
-    p.header->xl = (rep > 1) ? 1 : p.xl_flat;
+    p.header->error = (running > p.max_items) ? 1 : 0;
   }
 }
 
@@ -399,14 +296,6 @@ struct DecodeTraits {
   static constexpr int SLOT = 4 * kPageSize * RS;  // two pages of K and V in LDS
   // Pages in flight per wave (~128-160 registers of staging).
   static constexpr int NB = (D == 64) ? MI_DECODE_NB64 : (D == 128) ? MI_DECODE_NB128 : 2;
-  static constexpr int OUT = D / 64;  // merged outputs per head per lane (contiguous dims)
-  // A split's bf16 partial row of one head, for one lane: OUT dims in 2, 4
-  // or 8 bytes (one or two registers).
-  using Part = typename std::conditional<D == 64, uint16_t, typename std::conditional<D == 128, uint32_t, uint64_t>::type>::type;
-  static constexpr int PREGS = D == 256 ? 2 : 1;
-  // Splits whose partial rows one merge batch loads together (<= 96 registers).
-  static constexpr int KB_RAW = MI_DECODE_KB_REGS / (G * PREGS);
-  static constexpr int KB = KB_RAW > 16 ? 16 : (KB_RAW < 1 ? 1 : KB_RAW);
   static_assert(G >= 1 && G <= 16, "group size");
   static_assert((NB - 1) * 2 * LPI <= 63, "vmcnt range");
   static_assert(NB % 2 == 0, "pages are consumed in pairs");
@@ -446,19 +335,6 @@ __device__ __forceinline__ F coherent_load(const F* p) {
 template <typename F>
 __device__ __forceinline__ void coherent_store(F* p, F v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Split partials: device-coherent (bypassing the XCD's L2) in general, or
-// L2-coherent only when every unit of a (request, KV head) runs on one XCD
-// (XL), which keeps the publish / merge round trips inside that L2.
-template <bool XL, typename F>
-__device__ __forceinline__ F partial_load(const F* p) {
-  if constexpr (XL) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  else return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <bool XL, typename F>
-__device__ __forceinline__ void partial_store(F* p, F v) {
-  if constexpr (XL) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  else __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
@@ -538,9 +414,10 @@ __device__ __forceinline__ float group_sum(float x) {
 }
 
 // Split-K tail of a unit: publish the partial (O rows, m, l), count, and
-// the last unit of the (request, KV head) merges all splits.  XL: the
-// partials stay in the XCD's L2 (every split ran on this XCD), else they go
-// device-coherent (write-through, bypassing the L2 on the way back).
+// the last unit of the (request, KV head) merges all splits.  Partials are
+// written and read device-coherent (sc1: through to the memory side, so
+// splits on other XCDs see them; keeping them in one XCD's L2 when all
+// splits of a request share an XCD measured no faster).
 //
 // Partial O rows are bf16 in "lane order": position j * NT + t of a head's
 // row holds dim 16 t + j, which is what lane (g, j) of the MFMA accumulators
@@ -550,13 +427,13 @@ __device__ __forceinline__ float group_sum(float x) {
 // chunk l % LR; the splits' m and l are laid out the same way (lane l: head
 // l / LR of a row group, split l % LR of a split group), so the weight of
 // split s for a lane's head is a shuffle inside its LR-lane group.
-template <int D, int G, bool XL>
+template <int D, int G>
 __device__ __forceinline__ void publish_merge(const RunParams& p, int u, int b, int hkv, int nsplit, int item_base,
-                                              int stride, const mi::f32x4_t (&acc)[DecodeTraits<D, G>::NT],
-                                              float m_run, float lt) {
+                                              const mi::f32x4_t (&acc)[DecodeTraits<D, G>::NT], float m_run,
+                                              float lt) {
   using T = DecodeTraits<D, G>;
   constexpr int NT = T::NT;
-  constexpr int CP = XL ? 1 : 16;  // cache policy bits: sc0 (workgroup scope) / sc1 (device scope)
+  constexpr int CP = 16;  // cache policy: sc1 (device scope)
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, j = lane & 15;
   const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(p.po, (short)0, p.po_bytes, kBufferWord3);
@@ -601,7 +478,7 @@ __device__ __forceinline__ void publish_merge(const RunParams& p, int u, int b, 
   constexpr int LR = 64 / R;          // lanes per row
   constexpr int A = (G + R - 1) / R;  // row groups covering the G heads
   constexpr int C = 64 / LR;          // split groups per round of 64 splits
-  constexpr int KB = MI_DECODE_MERGE_KB;  // splits whose rows are loaded together
+  constexpr int KB = 8;  // splits whose rows are loaded together (16 measured slower)
   static_assert(LR % KB == 0, "batches inside a split group");
   const int hg = lane / LR, sg = lane % LR;
   float M[A], Lt[A], sum[A][8];
@@ -612,7 +489,7 @@ __device__ __forceinline__ void publish_merge(const RunParams& p, int u, int b, 
 #pragma unroll
     for (int k = 0; k < 8; ++k) sum[a][k] = 0.f;
   }
-  auto unit_of = [&](int s) { return (item_base + s * stride) * p.hkv + hkv; };
+  auto unit_of = [&](int s) { return (item_base + s) * p.hkv + hkv; };
   auto load_batch = [&](u32x4_t (&v)[KB][A], int s0, int nr) {
 #pragma unroll
     for (int q = 0; q < KB; ++q) {
@@ -726,7 +603,7 @@ __device__ __forceinline__ void publish_merge(const RunParams& p, int u, int b, 
 //                LDS transpose read (lane (g, j) gets V[4g..4g+3][16t + j]);
 //                O[head 4g+i][16t + j] accumulates in registers.
 template <int D, int G, int W, int NB>
-__device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, lds_t* wg_lds, bool xl) {
+__device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, lds_t* wg_lds) {
   using T = DecodeTraits<D, G>;
   using Regs = PageRegs<D, G>;
   static_assert((NB - 1) * 2 * T::LPI <= 63 && NB % 2 == 0, "vmcnt range; pages are consumed in pairs");
@@ -738,7 +615,6 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
   const int last_valid = mi::read_lane_i(iv, kItemLast);
   const int nsplit = mi::read_lane_i(iv, kItemNsplit);
   const int item_base = mi::read_lane_i(iv, kItemBase);
-  const int stride = mi::read_lane_i(iv, kItemStride);
   if (nsplit == 0) return;  // a padding item (the same for every wave of the workgroup)
   const int g = lane >> 4, j = lane & 15;
 
@@ -951,8 +827,7 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
     return;
   }
 
-  if (xl) publish_merge<D, G, true>(p, u, b, hkv, nsplit, item_base, stride, acc, m_run, lt);
-  else publish_merge<D, G, false>(p, u, b, hkv, nsplit, item_base, stride, acc, m_run, lt);
+  publish_merge<D, G>(p, u, b, hkv, nsplit, item_base, acc, m_run, lt);
 }
 
 // A workgroup of W waves runs units blockIdx * W + w, w < W: W consecutive
@@ -970,9 +845,6 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 128
   // way), so the reads are in flight together.
   int iv = load_item_word(p, u);
   const int num_units = p.header->num_units;
-  // plan() decides where split partials live: L2-local when every unit of a
-  // (request, KV head) runs on one XCD
-  const bool xl = p.header->xl != 0;
   // Short items (a few page pairs per unit) keep fewer pages in flight: the
   // first pages of every wave arrive sooner, the rest overlaps across waves.
   constexpr int NBL = DecodeTraits<D, G>::NB;
@@ -980,10 +852,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 128
   const bool short_items = NBS != NBL && p.header->chunk_pages <= MI_DECODE_SHORT_CHUNK;
   while (u < num_units) {
     if constexpr (NBS != NBL) {
-      if (short_items) decode_unit<D, G, W, NBS>(p, u, iv, lds, xl);
-      else decode_unit<D, G, W, NBL>(p, u, iv, lds, xl);
+      if (short_items) decode_unit<D, G, W, NBS>(p, u, iv, lds);
+      else decode_unit<D, G, W, NBL>(p, u, iv, lds);
     } else {
-      decode_unit<D, G, W, NBL>(p, u, iv, lds, xl);
+      decode_unit<D, G, W, NBL>(p, u, iv, lds);
     }
     u += int(gridDim.x) * W;
     if (u < num_units) iv = load_item_word(p, u);
@@ -1053,8 +925,6 @@ extern "C" int mi_decode_plan(void* workspace, size_t workspace_bytes, const int
   mi::clear_error();
   int rc = check_shape("decode plan", batch_size, num_qo_heads, num_kv_heads, head_dim, page_size);
   if (rc) return rc;
-  // learn the workgroup -> XCD mapping once per device (outside captures)
-  (void)mi::xcd_round_robin(static_cast<hipStream_t>(stream), true);
   if (max_units <= 0) max_units = units_that_fit(workspace_bytes, batch_size, num_qo_heads, num_kv_heads, head_dim);
   const DecodeLayout L = decode_layout(batch_size, num_qo_heads, num_kv_heads, head_dim, max_units);
   if (!workspace || workspace_bytes < L.total)
@@ -1073,19 +943,6 @@ extern "C" int mi_decode_plan(void* workspace, size_t workspace_bytes, const int
   pp.hkv = num_kv_heads;
   pp.target_units = mi::num_cus() * kUnitsPerCU;
   pp.max_items = L.max_items;
-  // Item classes: workgroup x runs on XCD x mod nx; unit u = item * kv_heads
-  // + h runs on workgroup u / W.  With k = kv_heads / W workgroups per item,
-  // all units of a (request, h) share an XCD when nx divides k, or when k
-  // divides nx and the request's items are all congruent mod nx / k.
-  const int waves = waves_per_group(head_dim, num_kv_heads);
-  const int nx = mi::xcd_round_robin(static_cast<hipStream_t>(stream), false);
-  const int k = num_kv_heads / waves;
-  pp.rep = 1;
-  pp.xl_flat = 0;
-  if (nx > 0 && run_grid(max_units, waves) % nx == 0) {
-    if (k % nx == 0) pp.xl_flat = 1;
-    else if (nx % k == 0 && nx / k <= kMaxRep) pp.rep = nx / k;
-  }
   pp.header = reinterpret_cast<DecodeHeader*>(ws);
   pp.items = reinterpret_cast<DecodeItem*>(ws + L.items);
   pp.counters = reinterpret_cast<int*>(ws + L.counters);
