@@ -193,7 +193,10 @@ __device__ int block_scan(int v, int* wsum, int* total) {
 __device__ __forceinline__ int request_pages(const PlanParams& p, int b) {
   return max(0, p.indptr[b + 1] - p.indptr[b]);
 }
-__device__ __forceinline__ int items_of(int np, int chunk) { return max(1, (np + chunk - 1) / chunk); }
+// Items of a request of np pages at q16 / 16 pages per item (q16 in 1/16
+// pages: a fractional item length lets the item count land close to the
+// limit, and items then hold floor or ceil of np / nsplit pages).
+__device__ __forceinline__ int items_of(int np, int q16) { return max(1, (np * 16 + q16 - 1) / q16); }
 
 __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
   __shared__ int red[16];
@@ -208,25 +211,26 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
   }
   const int max_np = block_max(mx, red);
   const long long total_np = block_sum(tot, red);
-  // Pages per item ("chunk"): the smallest value whose items fit the limit,
-  // found by binary search (the item count is non-increasing in chunk).  The
-  // limit is one resident round of units (target_units / kv_heads items), so
-  // no wave runs a second unit -- or whole rounds when the batch alone needs
-  // more -- and never more items than the workspace holds.
+  // Pages per item, in 1/16 pages ("q16"): the smallest value whose items
+  // fit the limit, found by binary search (the item count is non-increasing
+  // in q16).  The limit is one resident round of units (target_units /
+  // kv_heads items), so no wave runs a second unit -- or whole rounds when
+  // the batch alone needs more -- and never more items than the workspace
+  // holds.
   const int round_items = max(1, p.target_units / p.hkv);
   int limit = ((p.batch + round_items - 1) / round_items) * round_items;
   limit = min(max(limit, 1), p.max_items);
-  // every chunk below total / limit has more than `limit` items (each
-  // request has at least ceil(np / chunk) of them)
-  int hi = max(max_np, 1);
-  int lo = min(hi, max(1, int((total_np + limit - 1) / limit)));
+  // every q16 below 16 total / limit has more than `limit` items (each
+  // request has at least np * 16 / q16 of them)
+  int hi = 16 * max(max_np, 1);
+  int lo = min(hi, max(16, int((16 * total_np + limit - 1) / limit)));
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
     int cnt = 0;
     for (int b = t; b < p.batch; b += blockDim.x) cnt += items_of(request_pages(p, b), mid);
     if (block_sum(cnt, red) <= limit) hi = mid; else lo = mid + 1;
   }
-  const int chunk = lo;
+  const int q16 = lo;
   // Items, 1024 requests at a time: the scan gives each request's first
   // item, then every thread writes whole items (one item per thread per
   // round, its inline page ids loaded together), finding the item's request
@@ -238,7 +242,7 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
     if (b < p.batch) {
       pb0 = p.indptr[b];
       np = max(0, p.indptr[b + 1] - pb0);
-      ns = items_of(np, chunk);
+      ns = items_of(np, q16);
       lpl = min(max(p.last_page_len[b], 1), kPageSize);
     }
     s_np[t] = np;
@@ -280,7 +284,7 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
     const int items = min(running, p.max_items);
     p.header->num_items = items;
     p.header->num_units = items * p.hkv;
-    p.header->chunk_pages = chunk;
+    p.header->chunk_pages = (q16 + 15) / 16;  // the longest item
     p.header->error = (running > p.max_items) ? 1 : 0;
   }
 }
