@@ -44,8 +44,10 @@ namespace {
 
 constexpr int kPageSize = 16;
 constexpr float kLazyRescale = 8.0f;  // log2 units
+// Units (waves) per CU in the plan's resident round: 6 measured faster than 8
+// (fewer splits, so less partial traffic and shorter merges) and than 4, 5, 7.
 #ifndef MI_DECODE_UNITS_PER_CU
-#define MI_DECODE_UNITS_PER_CU 8
+#define MI_DECODE_UNITS_PER_CU 6
 #endif
 constexpr int kUnitsPerCU = MI_DECODE_UNITS_PER_CU;
 #ifndef MI_DECODE_NB128
@@ -838,7 +840,8 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
 // KV heads of one item (W divides kv_heads, and the unit count is a multiple
 // of kv_heads, so the waves of a workgroup run the same number of units).
 // head_dim <= 128: registers capped at 256 per wave, so at least two waves
-// share a SIMD (8 units per CU).  head_dim 256 needs the full register file.
+// share a SIMD (the plan's 6 units per CU fit).  head_dim 256 needs the full
+// register file.
 template <int D, int G, int W>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 128 ? MI_DECODE_WAVES : 1))) void decode_run_kernel(
     RunParams p) {
