@@ -34,9 +34,16 @@
 //                   transpose read in the same key order.
 #include <math.h>
 
+#include <type_traits>
+
 #include "mi_common.h"
 
 namespace {
+
+// s_waitcnt immediate (gfx9 encoding): vmcnt = 0, expcnt = 7, lgkmcnt = 15.
+constexpr int kWaitVmcnt0 = 0x0F70;
+// Buffer resource word 3 for gfx9 raw buffers (32-bit data format, no swizzle).
+constexpr int kBufferWord3 = 0x00020000;
 
 constexpr int kPageSize = 16;
 constexpr int kMinRows = 16;   // smallest query-position block per workgroup
@@ -252,9 +259,6 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
   const int pblocks = p.bm / 16;          // position blocks per head
   const int nrb = pblocks * p.group;      // row blocks of the workgroup
 
-  const int64_t tok_stride = int64_t(p.hkv) * D;
-  const int64_t kv_stride = kPageSize * tok_stride;
-  const int64_t page_stride = 2 * kv_stride;
 
   // ---- this wave's row blocks: rb = w, w + 4
   mi::bf16x8_t qb[T::MAXRB][T::KSTEPS];
@@ -301,46 +305,64 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
   block_hi = max(block_hi, 0);
   const int ntile = (block_hi + kKvTile - 1) / kKvTile;
 
-  // ---- staging.  Chunk c = thread + 256 i of a tile is token c / CPR, 16-byte
-  // chunk c % CPR.  Page ids are fetched one tile ahead of the K/V loads, so
-  // the loads never wait on an index load.
+  // ---- staging.  Load i of a thread covers token ltok + TPL i of the tile
+  // and 16-byte chunk ldc of that token's row: a wave's 64 lanes cover whole
+  // rows of one page (1 KB <= 16 rows), so the page id is wave-uniform -- a
+  // scalar load, fetched one tile ahead -- and each page gets a buffer
+  // descriptor (size 0 past the request's pages; on the request's last page
+  // the size stops after its valid V rows, so the V rows past kv_len read as
+  // zeros: P is 0 there, but 0 * NaN would poison the MFMA).  No address
+  // arithmetic or branches per load.
+  constexpr int TPL = T::THREADS / T::CPR;
+  const int ltok = int(threadIdx.x) / T::CPR, ldc = int(threadIdx.x) - ltok * T::CPR;
+  const int tok_bytes = p.hkv * D * 2;
+  const int kv_bytes = kPageSize * tok_bytes;
+  const int page_bytes = 2 * kv_bytes;
+  const int npages_req = (t.kv_len + kPageSize - 1) / kPageSize;
+  const int last_rows = t.kv_len - (npages_req - 1) * kPageSize;
+  int voff[T::LOADS], pit[T::LOADS];
+#pragma unroll
+  for (int i = 0; i < T::LOADS; ++i) {
+    const int tt = ltok + TPL * i;
+    pit[i] = __builtin_amdgcn_readfirstlane(tt / kPageSize);
+    voff[i] = (tt % kPageSize) * tok_bytes + hkv * D * 2 + ldc * 16;
+  }
   u32x4_t kreg[T::LOADS], vreg[T::LOADS];
   int pid[T::LOADS];
+  // page ids through the constant address space: a uniform index then
+  // compiles to a scalar load (kv_indices is not written during the launch)
+  typedef __attribute__((address_space(4))) const int32_t const_i32;
+  const const_i32* kv_ids = (const const_i32*)(p.indices);
   auto fetch_ids = [&](int kt) {
-    const int kv0 = kt * kKvTile;
 #pragma unroll
     for (int i = 0; i < T::LOADS; ++i) {
-      const int j = kv0 + (int(threadIdx.x) + T::THREADS * i) / T::CPR;
-      pid[i] = (kt < ntile && j < t.kv_len) ? p.indices[t.kv_page_begin + j / kPageSize] : -1;
+      const int pg_idx = kt * (kKvTile / kPageSize) + pit[i];
+      // the index is clamped into the request's pages (it has >= 1 page
+      // whenever there is a tile), then the id is dropped past the end
+      const int v = kv_ids[t.kv_page_begin + min(pg_idx, npages_req - 1)];
+      pid[i] = (kt < ntile && pg_idx < npages_req) ? v : -1;
     }
   };
   auto load_tile = [&](int kt) {
-    const int kv0 = kt * kKvTile;
 #pragma unroll
     for (int i = 0; i < T::LOADS; ++i) {
-      const int c = threadIdx.x + T::THREADS * i;
-      const int tok = c / T::CPR, dc = c - tok * T::CPR;
-      const int j = kv0 + tok;
-      u32x4_t kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
-      const int64_t page = pid[i];
-      if (page >= 0 && page < p.num_pages) {
-        const uint16_t* src = p.pool + page * page_stride + (j % kPageSize) * tok_stride + int64_t(hkv) * D + dc * 8;
-        kv = __builtin_bit_cast(u32x4_t, mi::load16(src));
-        vv = __builtin_bit_cast(u32x4_t, mi::load16(src + kv_stride));
-      }
-      kreg[i] = kv;
-      vreg[i] = vv;
+      const int pg = pid[i];
+      const bool ok = pg >= 0 && pg < p.num_pages;
+      const int pg_idx = kt * (kKvTile / kPageSize) + pit[i];
+      const int size = !ok ? 0 : (pg_idx == npages_req - 1 ? kv_bytes + last_rows * tok_bytes : page_bytes);
+      const char* base = reinterpret_cast<const char*>(p.pool) + (ok ? int64_t(pg) * page_bytes : 0);
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, size, kBufferWord3);
+      kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[i], 0, 0);
+      vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[i], kv_bytes, 0);
     }
   };
   auto store_tile = [&](int buf) {
-    lds_t* kl = lds + buf * 2 * T::TILE;
+    lds_t* kl = lds + buf * 2 * T::TILE + ltok * T::RS + ldc * 16;
     lds_t* vl = kl + T::TILE;
 #pragma unroll
     for (int i = 0; i < T::LOADS; ++i) {
-      const int c = threadIdx.x + T::THREADS * i;
-      const int tok = c / T::CPR, dc = c - tok * T::CPR;
-      lds_store16(kl + tok * T::RS + dc * 16, kreg[i]);
-      lds_store16(vl + tok * T::RS + dc * 16, vreg[i]);
+      lds_store16(kl + TPL * i * T::RS, kreg[i]);
+      lds_store16(vl + TPL * i * T::RS, vreg[i]);
     }
   };
 
@@ -350,6 +372,11 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
     fetch_ids(1);
     store_tile(0);
   }
+  // Everything loaded so far (Q, tile 0, the next page ids) is waited for
+  // here, so the loop head carries no pending load from before the loop;
+  // without it the compiler put a full vmcnt(0) before the first score MFMA
+  // of every tile, which also waited for the next tile's prefetch.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
 
   for (int kt = 0; kt < ntile; ++kt) {
@@ -376,28 +403,33 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
       // ---- S^T for the tile's four 16-key blocks (raw scores; the softmax
       // scale is applied inside the exponent)
       float sv[T::MAXRB][4][4];
+      // two copies of the score loop, so full tiles carry no mask code
+      auto scores = [&](auto masked) {
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        mi::bf16x8_t ka[T::KSTEPS];
+        for (int kb = 0; kb < 4; ++kb) {
+          mi::bf16x8_t ka[T::KSTEPS];
 #pragma unroll
-        for (int s = 0; s < T::KSTEPS; ++s)
-          ka[s] = __builtin_bit_cast(mi::bf16x8_t, lds_load16(kl + (kb * 16 + n) * T::RS + (4 * s + g) * 16));
+          for (int s = 0; s < T::KSTEPS; ++s)
+            ka[s] = __builtin_bit_cast(mi::bf16x8_t, lds_load16(kl + (kb * 16 + n) * T::RS + (4 * s + g) * 16));
 #pragma unroll
-        for (int r = 0; r < T::MAXRB; ++r) {
-          mi::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+          for (int r = 0; r < T::MAXRB; ++r) {
+            mi::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int s = 0; s < T::KSTEPS; ++s) c = mi::mfma_16x16x32_bf16(ka[s], qb[r][s], c);
+            for (int s = 0; s < T::KSTEPS; ++s) c = mi::mfma_16x16x32_bf16(ka[s], qb[r][s], c);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) sv[r][kb][i] = c[i];
-          if (!full) {
-            // key kv0 + kb*16 + 4g + i is visible iff kb*16 + i <= lim - kv0 - 4g
-            const int rel = lim[r] - kv0 - 4 * g;
+            for (int i = 0; i < 4; ++i) sv[r][kb][i] = c[i];
+            if constexpr (decltype(masked)::value) {
+              // key kv0 + kb*16 + 4g + i is visible iff kb*16 + i <= lim - kv0 - 4g
+              const int rel = lim[r] - kv0 - 4 * g;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (kb * 16 + i > rel) sv[r][kb][i] = -INFINITY;
+              for (int i = 0; i < 4; ++i)
+                if (kb * 16 + i > rel) sv[r][kb][i] = -INFINITY;
+            }
           }
         }
-      }
+      };
+      if (full) scores(std::false_type{});
+      else scores(std::true_type{});
       // ---- online softmax per row, lazy rescale; P packed as the A operand
       mi::bf16x8_t pa[T::MAXRB][2];
 #pragma unroll
