@@ -57,6 +57,9 @@ def test_config1_qwen05_heads(dev):
     (12, 2, 128),   # group 6
     (4, 2, 64),     # group 2
     (16, 4, 256),   # head_dim 256
+    (6, 3, 128),    # odd kv_heads: one-wave workgroups
+    (8, 1, 128),    # one KV head (MQA), group 8
+    (4, 1, 64),     # one KV head, head_dim 64
 ])
 def test_shapes_ragged(dev, hq, hkv, d):
     lens = [1, 15, 16, 17, 33, 100, 257, 700]
@@ -213,3 +216,20 @@ def test_golden_fixture_config1(dev):
     w.plan(t["indptr"].to(dev), t["page_ids"].to(dev), t["last_page_len"].to(dev), 14, 2, 64, 16)
     out = w.run(t["q"].to(dev), load_pool(t).to(dev)).float().cpu()
     assert (out - t["out_fp32"]).abs().max().item() < TOL
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64), (6, 3, 128)])
+def test_stale_rows_past_the_end_are_not_read(dev, hq, hkv, d):
+    """NaN in every pool row past each request's length on its last page."""
+    lens = [37, 100, 5, 250, 1000]
+    b = make_paged_batch(lens, hq, hkv, d, seed=22)
+    pool = b["pool"].clone()
+    idx = b["indices"].tolist()
+    for r in range(len(lens)):
+        hi = b["indptr"][r + 1]
+        if b["last"][r] < 16:
+            pool[idx[hi - 1], :, b["last"][r]:] = float("nan")
+    b = {**b, "pool": pool}
+    out = _decode(dev, b, hq, hkv, d)
+    assert torch.isfinite(out).all()
+    assert (out - _ref(b)).abs().max().item() < TOL

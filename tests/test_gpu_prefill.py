@@ -38,7 +38,8 @@ def _run(dev, b, qo_lens, hq, hkv, d, causal=True, seed=0):
     return out.float().cpu(), ref
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (32, 8, 128), (28, 4, 128), (64, 8, 128)])
+@pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (32, 8, 128), (28, 4, 128), (64, 8, 128),
+                                      (6, 3, 128), (8, 1, 64), (16, 4, 256)])
 @pytest.mark.parametrize("L", [1, 5, 64, 100, 300])
 def test_single_request_causal(dev, hq, hkv, d, L):
     b = make_paged_batch([L], hq, hkv, d, seed=L + d)
@@ -94,3 +95,24 @@ def test_prefill_then_decode_consistency(dev):
            torch.tensor(b["last"], dtype=torch.int32, device=dev), 32, 8, 128, 16)
     dec = w.run(last_q.to(dev), b["pool"].to(dev)).float().cpu()
     assert (dec - torch.stack([out[76], out[77 + 129]])).abs().max().item() < TOL
+
+
+def _poison_tails(b):
+    """NaN in every row past each request's length on its last page (K and V),
+    where a pool holds stale data in practice; no result may read them."""
+    pool = b["pool"].clone()
+    idx = b["indices"].tolist()
+    for r in range(len(b["last"])):
+        lo, hi = b["indptr"][r], b["indptr"][r + 1]
+        if hi > lo and b["last"][r] < 16:
+            pool[idx[hi - 1], :, b["last"][r]:] = float("nan")
+    return {**b, "pool": pool}
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64)])
+def test_stale_rows_past_the_end_are_not_read(dev, hq, hkv, d):
+    lens = [37, 100, 5, 250]
+    b = _poison_tails(make_paged_batch(lens, hq, hkv, d, seed=21))
+    out, ref = _run(dev, b, lens, hq, hkv, d, seed=21)
+    assert torch.isfinite(out).all()
+    assert (out - ref).abs().max().item() < TOL
