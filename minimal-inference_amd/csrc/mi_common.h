@@ -38,6 +38,18 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
 }
+// The same rounding (to nearest even) in one gfx950 instruction
+// (v_cvt_pk_bf16_f32) per pair, for kernel outputs: finite values convert
+// bit-identically to f32_to_bf16; a NaN comes out as a quiet NaN.
+typedef __attribute__((ext_vector_type(2))) float f32x2_hw;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_hw;
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_hw){lo, hi}, bf16x2_hw));
+}
+__device__ __forceinline__ uint16_t cvt_bf16(float f) { return uint16_t(cvt_pk_bf16(f, 0.f)); }
+// 1 / x by the hardware reciprocal (1 ulp), for normalising outputs that are
+// rounded to bf16 anyway.
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
 // ---------------------------------------------------------------- MFMA types
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;

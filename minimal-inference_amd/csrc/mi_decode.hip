@@ -451,7 +451,7 @@ __device__ __forceinline__ void publish_merge(const RunParams& p, int u, int b, 
       if (h < G) {
         uint32_t w[NT / 2];
 #pragma unroll
-        for (int t = 0; t < NT / 2; ++t) w[t] = mi::pack_bf16x2(acc[2 * t][i], acc[2 * t + 1][i]);
+        for (int t = 0; t < NT / 2; ++t) w[t] = mi::cvt_pk_bf16(acc[2 * t][i], acc[2 * t + 1][i]);
         const int off = (u * G + h) * D * 2 + j * NT * 2;
         if constexpr (NT == 4) {
           __builtin_amdgcn_raw_buffer_store_b64((__attribute__((ext_vector_type(2))) unsigned int){w[0], w[1]}, rpo, off, 0, CP);
@@ -579,12 +579,12 @@ __device__ __forceinline__ void publish_merge(const RunParams& p, int u, int b, 
   for (int a = 0; a < A; ++a) {
     const int h = a * R + hg;
     if (h < G) {
-      const float inv = Lt[a] > 0.f ? 1.f / Lt[a] : 0.f;
+      const float inv = Lt[a] > 0.f ? mi::fast_rcp(Lt[a]) : 0.f;
       uint16_t* orow = p.out + int64_t(b) * p.o_sb + int64_t(hkv * G + h) * p.o_sh;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const int pos = sg * 8 + k;
-        orow[16 * (pos % NT) + pos / NT] = mi::f32_to_bf16(sum[a][k] * inv);
+        orow[16 * (pos % NT) + pos / NT] = mi::cvt_bf16(sum[a][k] * inv);
       }
     }
   }
@@ -824,10 +824,10 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
     for (int i = 0; i < 4; ++i) {
       const int h = 4 * g + i;
       if (h < G) {
-        const float inv = lo[i] > 0.f ? 1.f / lo[i] : 0.f;
+        const float inv = lo[i] > 0.f ? mi::fast_rcp(lo[i]) : 0.f;
         uint16_t* orow = p.out + int64_t(b) * p.o_sb + int64_t(hkv * G + h) * p.o_sh + j;
 #pragma unroll
-        for (int t = 0; t < T::NT; ++t) orow[16 * t] = mi::f32_to_bf16(acc[t][i] * inv);
+        for (int t = 0; t < T::NT; ++t) orow[16 * t] = mi::cvt_bf16(acc[t][i] * inv);
       }
     }
     return;

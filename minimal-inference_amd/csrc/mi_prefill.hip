@@ -269,6 +269,8 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
   int rb_hi[T::MAXRB];    // keys this row block needs (causal)
   int head[T::MAXRB];
   int nblk = 0;
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.q + int64_t(t.q_begin) * p.q_st), (short)0, int(int64_t(t.q_rows) * p.q_st * 2), kBufferWord3);
 #pragma unroll
   for (int r = 0; r < T::MAXRB; ++r) {
     const int rb = w + T::WAVES * r;
@@ -283,13 +285,12 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
     lim[r] = !valid ? -1 : (p.causal ? min(t.kv_len - 1, qpos[r] + off) : t.kv_len - 1);
     const int last = t.row0 + min(pb * 16 + 15, t.q_rows - 1);
     rb_hi[r] = !has ? 0 : (p.causal ? min(t.kv_len, last + off + 1) : t.kv_len);
-    const uint16_t* qrow = p.q + int64_t(t.q_begin + (valid ? local : 0)) * p.q_st + int64_t(head[r]) * p.q_sh + g * 8;
+    // Q rows through a descriptor over the tile's rows: a row past the tile
+    // reads out of range (zeros), so the loads are unconditional
+    const int qoff = valid ? int((int64_t(local) * p.q_st + int64_t(head[r]) * p.q_sh + g * 8) * 2) : 0x7ffffff0;
 #pragma unroll
-    for (int s = 0; s < T::KSTEPS; ++s) {
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (valid) v = mi::load16(qrow + s * 32);
-      qb[r][s] = mi::as_bf16x8(v);
-    }
+    for (int s = 0; s < T::KSTEPS; ++s)
+      qb[r][s] = __builtin_bit_cast(mi::bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(rq, qoff, s * 64, 0));
 #pragma unroll
     for (int j = 0; j < T::NT; ++j) o[r][j] = mi::f32x4_t{0.f, 0.f, 0.f, 0.f};
     m_run[r] = -INFINITY;
@@ -504,12 +505,12 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float li = mi::lane_shuffle(lt, 4 * g + i);
-      const float inv = li > 0.f ? 1.f / li : 0.f;
+      const float inv = li > 0.f ? mi::fast_rcp(li) : 0.f;
       const int local = pb * 16 + 4 * g + i;
       if (local < t.q_rows && t.q_begin + local < p.total_q) {
         uint16_t* orow = p.out + int64_t(t.q_begin + local) * p.o_st + int64_t(head[r]) * p.o_sh;
 #pragma unroll
-        for (int j = 0; j < T::NT; ++j) orow[j * 16 + n] = mi::f32_to_bf16(o[r][j][i] * inv);
+        for (int j = 0; j < T::NT; ++j) orow[j * 16 + n] = mi::cvt_bf16(o[r][j][i] * inv);
       }
     }
   }
