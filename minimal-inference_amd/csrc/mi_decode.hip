@@ -735,15 +735,19 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
     mloc = max_xor32(mloc);
     const bool need = mloc > m_run + kLazyRescale;
     if (__builtin_amdgcn_ballot_w64(need)) {
-      const float mnew = need ? mloc : m_run;
-      const float f = need ? ((m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - mnew)) : 1.f;
-      m_run = mnew;
+      // a head that has seen no token yet (m_run = -inf) still has O = 0 and
+      // l = 0: only its max moves, nothing is rescaled
+      const bool scale = need && m_run != -INFINITY;
+      const float f = scale ? __builtin_amdgcn_exp2f(m_run - mloc) : 1.f;
+      m_run = need ? mloc : m_run;
       l_run *= f;
+      if (__builtin_amdgcn_ballot_w64(scale)) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float fo = mi::lane_shuffle(f, 4 * g + i);
+        for (int i = 0; i < 4; ++i) {
+          const float fo = mi::lane_shuffle(f, 4 * g + i);
 #pragma unroll
-        for (int t = 0; t < T::NT; ++t) acc[t][i] *= fo;
+          for (int t = 0; t < T::NT; ++t) acc[t][i] *= fo;
+        }
       }
     }
     // exp2(-inf - m) = 0 for masked tokens; m is taken as 0 while no token

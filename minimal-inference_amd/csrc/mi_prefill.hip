@@ -443,15 +443,19 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
         mloc = max_xor32(max_xor16(mloc)) * p.scale_log2;  // scale > 0 keeps the arg max
         const bool need = mloc > m_run[r] + kLazyRescale;
         if (__builtin_amdgcn_ballot_w64(need)) {
-          const float mnew = need ? mloc : m_run[r];
-          const float f = need ? ((m_run[r] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[r] - mnew)) : 1.f;
-          m_run[r] = mnew;
+          // a row that has seen no key yet (m_run = -inf) still has O = 0 and
+          // l = 0: only its max moves, nothing is rescaled
+          const bool scale = need && m_run[r] != -INFINITY;
+          const float f = scale ? __builtin_amdgcn_exp2f(m_run[r] - mloc) : 1.f;
+          m_run[r] = need ? mloc : m_run[r];
           l_run[r] *= f;
+          if (__builtin_amdgcn_ballot_w64(scale)) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float fo = mi::lane_shuffle(f, 4 * g + i);
+            for (int i = 0; i < 4; ++i) {
+              const float fo = mi::lane_shuffle(f, 4 * g + i);
 #pragma unroll
-            for (int j = 0; j < T::NT; ++j) o[r][j][i] *= fo;
+              for (int j = 0; j < T::NT; ++j) o[r][j][i] *= fo;
+            }
           }
         }
         // exp2(-inf - m) = 0 for masked keys; m is taken as 0 while the row
