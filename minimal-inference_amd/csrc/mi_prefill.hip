@@ -401,10 +401,12 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
       // to the wave's first valid row.  (Rows past the tile's end hold zero
       // queries and are never written, so they need no mask either.)
       const bool full = kv0 + kKvTile <= t.kv_len && (!p.causal || kv0 + kKvTile - 1 <= qmin + off);
-      // ---- S^T for the tile's four 16-key blocks (raw scores; the softmax
-      // scale is applied inside the exponent)
+      // ---- one tile: S^T for the four 16-key blocks (raw scores; the softmax
+      // scale is applied inside the exponent; two copies of the score loop,
+      // so full tiles carry no mask code), the row maxima, one lazy-rescale
+      // branch for the wave, then exp / pack / P V half by half, so the P V
+      // MFMAs of keys 0-31 can overlap the exponentials of keys 32-63.
       float sv[T::MAXRB][4][4];
-      // two copies of the score loop, so full tiles carry no mask code
       auto scores = [&](auto masked) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
@@ -431,67 +433,74 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
       };
       if (full) scores(std::false_type{});
       else scores(std::true_type{});
-      // ---- online softmax per row, lazy rescale; P packed as the A operand
-      mi::bf16x8_t pa[T::MAXRB][2];
+      {
+        float mloc[T::MAXRB];
+        bool need[T::MAXRB];
+        bool any_need = false;
 #pragma unroll
-      for (int r = 0; r < T::MAXRB; ++r) {
-        float mloc = sv[r][0][0];
+        for (int r = 0; r < T::MAXRB; ++r) {
+          float m = sv[r][0][0];
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+          for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) mloc = fmaxf(mloc, sv[r][kb][i]);
-        mloc = max_xor32(max_xor16(mloc)) * p.scale_log2;  // scale > 0 keeps the arg max
-        const bool need = mloc > m_run[r] + kLazyRescale;
-        if (__builtin_amdgcn_ballot_w64(need)) {
-          // a row that has seen no key yet (m_run = -inf) still has O = 0 and
-          // l = 0: only its max moves, nothing is rescaled
-          const bool scale = need && m_run[r] != -INFINITY;
-          const float f = scale ? __builtin_amdgcn_exp2f(m_run[r] - mloc) : 1.f;
-          m_run[r] = need ? mloc : m_run[r];
-          l_run[r] *= f;
-          if (__builtin_amdgcn_ballot_w64(scale)) {
+            for (int i = 0; i < 4; ++i) m = fmaxf(m, sv[r][kb][i]);
+          mloc[r] = max_xor32(max_xor16(m)) * p.scale_log2;  // scale > 0 keeps the arg max
+          need[r] = mloc[r] > m_run[r] + kLazyRescale;
+          any_need = any_need || need[r];
+        }
+        if (__builtin_amdgcn_ballot_w64(any_need)) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float fo = mi::lane_shuffle(f, 4 * g + i);
+          for (int r = 0; r < T::MAXRB; ++r) {
+            // a row that has seen no key yet (m_run = -inf) still has O = 0
+            // and l = 0: only its max moves, nothing is rescaled
+            const bool scale = need[r] && m_run[r] != -INFINITY;
+            const float f = scale ? __builtin_amdgcn_exp2f(m_run[r] - mloc[r]) : 1.f;
+            m_run[r] = need[r] ? mloc[r] : m_run[r];
+            l_run[r] *= f;
+            if (__builtin_amdgcn_ballot_w64(scale)) {
 #pragma unroll
-              for (int j = 0; j < T::NT; ++j) o[r][j][i] *= fo;
+              for (int i = 0; i < 4; ++i) {
+                const float fo = mi::lane_shuffle(f, 4 * g + i);
+#pragma unroll
+                for (int j = 0; j < T::NT; ++j) o[r][j][i] *= fo;
+              }
             }
           }
         }
-        // exp2(-inf - m) = 0 for masked keys; m is taken as 0 while the row
-        // has seen no key (m_run still -inf), avoiding -inf - -inf
-        const float m_use = (m_run[r] == -INFINITY) ? 0.f : m_run[r];
-        float pv[4][4];
-        float ps = 0.f;
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+        for (int h = 0; h < 2; ++h) {
+          // exp2(-inf - m) = 0 for masked keys; m is taken as 0 while the row
+          // has seen no key (m_run still -inf), avoiding -inf - -inf
+          mi::bf16x8_t pa[T::MAXRB];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            pv[kb][i] = __builtin_amdgcn_exp2f(fmaf(sv[r][kb][i], p.scale_log2, -m_use));
-            ps += pv[kb][i];
+          for (int r = 0; r < T::MAXRB; ++r) {
+            const float m_use = (m_run[r] == -INFINITY) ? 0.f : m_run[r];
+            float pv[2][4];
+            float ps = 0.f;
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                pv[kk][i] = __builtin_amdgcn_exp2f(fmaf(sv[r][2 * h + kk][i], p.scale_log2, -m_use));
+                ps += pv[kk][i];
+              }
+            l_run[r] += ps;
+            pa[r] = __builtin_bit_cast(
+                mi::bf16x8_t, __builtin_convertvector((f32x8_v){pv[0][0], pv[0][1], pv[0][2], pv[0][3], pv[1][0],
+                                                                pv[1][1], pv[1][2], pv[1][3]},
+                                                      bf16x8_v));
           }
-        l_run[r] += ps;
+          // ---- O += P V over key blocks (2h, 2h + 1)
+          const lds_t* v0 = vl + (2 * h * 16 + 4 * g + (n >> 2)) * T::RS + (n & 3) * 8;
+          const lds_t* v1 = v0 + 16 * T::RS;
 #pragma unroll
-        for (int pr = 0; pr < 2; ++pr)
-          pa[r][pr] = __builtin_bit_cast(
-              mi::bf16x8_t,
-              __builtin_convertvector((f32x8_v){pv[2 * pr][0], pv[2 * pr][1], pv[2 * pr][2], pv[2 * pr][3],
-                                                pv[2 * pr + 1][0], pv[2 * pr + 1][1], pv[2 * pr + 1][2],
-                                                pv[2 * pr + 1][3]},
-                                      bf16x8_v));
-      }
-      // ---- O += P V over key blocks (0, 1) and (2, 3)
+          for (int j = 0; j < T::NT; ++j) {
+            const s16x4_t a = lds_read_tr16(v0 + 32 * j), b = lds_read_tr16(v1 + 32 * j);
+            const mi::bf16x8_t vb =
+                __builtin_bit_cast(mi::bf16x8_t, (s16x8_t){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]});
 #pragma unroll
-      for (int pr = 0; pr < 2; ++pr) {
-        const lds_t* v0 = vl + (2 * pr * 16 + 4 * g + (n >> 2)) * T::RS + (n & 3) * 8;
-        const lds_t* v1 = v0 + 16 * T::RS;
-#pragma unroll
-        for (int j = 0; j < T::NT; ++j) {
-          const s16x4_t a = lds_read_tr16(v0 + 32 * j), b = lds_read_tr16(v1 + 32 * j);
-          const mi::bf16x8_t vb =
-              __builtin_bit_cast(mi::bf16x8_t, (s16x8_t){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]});
-#pragma unroll
-          for (int r = 0; r < T::MAXRB; ++r) o[r][j] = mi::mfma_16x16x32_bf16(pa[r][pr], vb, o[r][j]);
+            for (int r = 0; r < T::MAXRB; ++r) o[r][j] = mi::mfma_16x16x32_bf16(pa[r], vb, o[r][j]);
+          }
         }
       }
     }
