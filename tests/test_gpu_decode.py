@@ -233,3 +233,15 @@ def test_stale_rows_past_the_end_are_not_read(dev, hq, hkv, d):
     out = _decode(dev, b, hq, hkv, d)
     assert torch.isfinite(out).all()
     assert (out - _ref(b)).abs().max().item() < TOL
+
+
+@pytest.mark.parametrize("B,hq,hkv,d,max_ctx", [
+    (700, 32, 8, 128, 80),   # units > one resident round: the run's grid-stride rounds
+    (1100, 8, 2, 64, 40),    # more requests than the plan's 1024-thread scan takes at once
+])
+def test_large_batches(dev, B, hq, hkv, d, max_ctx):
+    g = torch.Generator().manual_seed(B)
+    lens = torch.randint(1, max_ctx + 1, (B,), generator=g).tolist()
+    b = make_paged_batch(lens, hq, hkv, d, seed=B)
+    err = (_decode(dev, b, hq, hkv, d) - _ref(b)).abs().max().item()
+    assert err < TOL, err
