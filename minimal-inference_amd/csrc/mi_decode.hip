@@ -50,6 +50,9 @@ constexpr float kLazyRescale = 8.0f;  // log2 units
 #define MI_DECODE_UNITS_PER_CU 6
 #endif
 constexpr int kUnitsPerCU = MI_DECODE_UNITS_PER_CU;
+#ifndef MI_DECODE_MERGE_BUDGET
+#define MI_DECODE_MERGE_BUDGET 40  // average splits x group per (request, KV head) the plan aims under
+#endif
 #ifndef MI_DECODE_NB128
 #define MI_DECODE_NB128 4
 #endif
@@ -952,7 +955,15 @@ extern "C" int mi_decode_plan(void* workspace, size_t workspace_bytes, const int
   pp.last_page_len = kv_last_page_len;
   pp.batch = batch_size;
   pp.hkv = num_kv_heads;
-  pp.target_units = mi::num_cus() * kUnitsPerCU;
+  // One resident round of units, but at most ~40 / group splits per
+  // (request, KV head) on average: the merge's cost grows with splits x
+  // group (Qwen2.5-7B, group 7: 4 units per CU instead of 6 took ~1 us off).
+  {
+    const int group = num_qo_heads / num_kv_heads;
+    const long long cap = (long long)(MI_DECODE_MERGE_BUDGET / group) * batch_size * num_kv_heads;
+    const int round = mi::num_cus() * kUnitsPerCU;
+    pp.target_units = int(cap < round ? (cap > mi::num_cus() * 2 ? cap : mi::num_cus() * 2) : round);
+  }
   pp.max_items = L.max_items;
   pp.header = reinterpret_cast<DecodeHeader*>(ws);
   pp.items = reinterpret_cast<DecodeItem*>(ws + L.items);
