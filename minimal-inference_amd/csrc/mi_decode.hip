@@ -50,6 +50,9 @@ constexpr float kLazyRescale = 8.0f;  // log2 units
 #define MI_DECODE_UNITS_PER_CU 6
 #endif
 constexpr int kUnitsPerCU = MI_DECODE_UNITS_PER_CU;
+#ifndef MI_DECODE_MIN_CHUNK
+#define MI_DECODE_MIN_CHUNK 4  // pages per item at least (2, 4, 8: 4 measured best on short contexts)
+#endif
 #ifndef MI_DECODE_MERGE_BUDGET
 #define MI_DECODE_MERGE_BUDGET 40  // average splits x group per (request, KV head) the plan aims under
 #endif
@@ -228,7 +231,9 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
   // every q16 below 16 total / limit has more than `limit` items (each
   // request has at least np * 16 / q16 of them)
   int hi = 16 * max(max_np, 1);
-  int lo = min(hi, max(16, int((16 * total_np + limit - 1) / limit)));
+  // Items of fewer than MI_DECODE_MIN_CHUNK pages only add merge work: the
+  // splits of short contexts do not need that much parallelism.
+  int lo = min(hi, max(16 * MI_DECODE_MIN_CHUNK, int((16 * total_np + limit - 1) / limit)));
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
     int cnt = 0;
