@@ -56,17 +56,14 @@ constexpr int kUnitsPerCU = MI_DECODE_UNITS_PER_CU;
 #ifndef MI_DECODE_MERGE_BUDGET
 #define MI_DECODE_MERGE_BUDGET 40  // average splits x group per (request, KV head) the plan aims under
 #endif
+// Pages in flight per wave: two for head_dim 128 (one page pair; four
+// measured slower on every decode shape here since the workgroups load
+// together), four for 64.
 #ifndef MI_DECODE_NB128
-#define MI_DECODE_NB128 4
-#endif
-#ifndef MI_DECODE_NB128_SHORT
-#define MI_DECODE_NB128_SHORT 2
-#endif
-#ifndef MI_DECODE_SHORT_CHUNK
-#define MI_DECODE_SHORT_CHUNK 8
+#define MI_DECODE_NB128 2
 #endif
 #ifndef MI_DECODE_NB64
-#define MI_DECODE_NB64 8
+#define MI_DECODE_NB64 4
 #endif
 #ifndef MI_DECODE_WAVES
 #define MI_DECODE_WAVES 2
@@ -864,18 +861,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 128
   // way), so the reads are in flight together.
   int iv = load_item_word(p, u);
   const int num_units = p.header->num_units;
-  // Short items (a few page pairs per unit) keep fewer pages in flight: the
-  // first pages of every wave arrive sooner, the rest overlaps across waves.
-  constexpr int NBL = DecodeTraits<D, G>::NB;
-  constexpr int NBS = (D == 128) ? MI_DECODE_NB128_SHORT : NBL;
-  const bool short_items = NBS != NBL && p.header->chunk_pages <= MI_DECODE_SHORT_CHUNK;
   while (u < num_units) {
-    if constexpr (NBS != NBL) {
-      if (short_items) decode_unit<D, G, W, NBS>(p, u, iv, lds);
-      else decode_unit<D, G, W, NBL>(p, u, iv, lds);
-    } else {
-      decode_unit<D, G, W, NBL>(p, u, iv, lds);
-    }
+    decode_unit<D, G, W, DecodeTraits<D, G>::NB>(p, u, iv, lds);
     u += int(gridDim.x) * W;
     if (u < num_units) iv = load_item_word(p, u);
   }
