@@ -60,6 +60,10 @@ constexpr float kLazyRescale = 8.0f;
 #define PREFILL_RS_PAD 32
 #endif
 // Row blocks of 16 per wave for head_dim 64 / 128 (256: always 1).
+// Output staging: pad bytes after every 8 columns (32 bytes each) of a
+// column-major 16-row block, so the 8-byte writes of a half wave and the
+// transpose reads of two lane groups fall on distinct banks.
+constexpr int kOutPad = 144;
 #ifndef PREFILL_MAXRB
 #define PREFILL_MAXRB 2
 #endif
@@ -198,7 +202,10 @@ typedef __attribute__((ext_vector_type(8))) float f32x8_v;
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_v;
 typedef __attribute__((address_space(3))) char lds_t;
 
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2_t;
+
 __device__ __forceinline__ void lds_store16(lds_t* p, u32x4_t v) { *(__attribute__((address_space(3))) u32x4_t*)p = v; }
+__device__ __forceinline__ void lds_store8(lds_t* p, u32x2_t v) { *(__attribute__((address_space(3))) u32x2_t*)p = v; }
 __device__ __forceinline__ u32x4_t lds_load16(const lds_t* p) {
   return *(const __attribute__((address_space(3))) u32x4_t*)p;
 }
@@ -268,6 +275,7 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
   int lim[T::MAXRB];      // last key this lane's row may see (-1: none)
   int rb_hi[T::MAXRB];    // keys this row block needs (causal)
   int head[T::MAXRB];
+  int pbk[T::MAXRB];      // position block of the row block
   int nblk = 0;
   const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.q + int64_t(t.q_begin) * p.q_st), (short)0, int(int64_t(t.q_rows) * p.q_st * 2), kBufferWord3);
@@ -279,6 +287,7 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
     const int hg = has ? rb / pblocks : 0;
     const int pb = has ? rb - hg * pblocks : 0;
     head[r] = hkv * p.group + hg;
+    pbk[r] = pb;
     const int local = pb * 16 + n;
     const bool valid = has && local < t.q_rows;
     qpos[r] = valid ? t.row0 + local : -1;
@@ -508,23 +517,53 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
     __syncthreads();
   }
 
-  // ---- normalise and store: lane (g, n) holds rows 4g + i, column 16j + n
+  // ---- normalise and store.  Lane (g, n) holds O rows 4g + i, columns 16j + n.
+  // The normalised rows go through LDS (the K / V buffers are free after the
+  // loop's last barrier) as a column-major block per row block: element
+  // (row, col) at byte col * 32 + (col / 8) * kOutPad + row * 2, so a lane's
+  // four rows of one column are one 8-byte write, and the LDS transpose read
+  // of a 4-column x 16-row block hands lane n four consecutive columns of row
+  // n: two reads give 16 contiguous bytes of an output row, one 16-byte store
+  // through a descriptor over the tile's output rows (rows past the tile get
+  // an out-of-range offset, so the stores are unconditional).
+  constexpr int kOutBlk = 8 * 32 + kOutPad;  // bytes per 8 columns
+  constexpr int OB = D / 8 * kOutBlk;        // bytes per row block
+  static_assert(T::WAVES * T::MAXRB * OB <= 2 * 2 * T::TILE, "output staging fits the K / V buffers");
+  lds_t* const ob = lds + w * T::MAXRB * OB;
+  const int wcol = n * 32 + (n >> 3) * kOutPad + 8 * g;
 #pragma unroll
   for (int r = 0; r < T::MAXRB; ++r) {
     if (r >= nblk) continue;
     const float lt = sum_xor32(sum_xor16(l_run[r]));
-    const int rb = w + T::WAVES * r;
-    const int pb = rb - (rb / pblocks) * pblocks;
+    float inv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float li = mi::lane_shuffle(lt, 4 * g + i);
-      const float inv = li > 0.f ? mi::fast_rcp(li) : 0.f;
-      const int local = pb * 16 + 4 * g + i;
-      if (local < t.q_rows && t.q_begin + local < p.total_q) {
-        uint16_t* orow = p.out + int64_t(t.q_begin + local) * p.o_st + int64_t(head[r]) * p.o_sh;
+      inv[i] = li > 0.f ? mi::fast_rcp(li) : 0.f;
+    }
 #pragma unroll
-        for (int j = 0; j < T::NT; ++j) orow[j * 16 + n] = mi::cvt_bf16(o[r][j][i] * inv);
-      }
+    for (int j = 0; j < T::NT; ++j)  // column 16j + n: 8-column block 2j + n / 8
+      lds_store8(ob + r * OB + j * 2 * kOutBlk + wcol,
+                 u32x2_t{mi::cvt_pk_bf16(o[r][j][0] * inv[0], o[r][j][1] * inv[1]),
+                         mi::cvt_pk_bf16(o[r][j][2] * inv[2], o[r][j][3] * inv[3])});
+  }
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.out + int64_t(t.q_begin) * p.o_st), (short)0, int(int64_t(t.q_rows) * p.o_st * 2), kBufferWord3);
+  // lane (g, n) reads columns 32q + 8g + [0, 8) of row n
+  const int rcol = g * kOutBlk + (n >> 2) * 32 + (n & 3) * 8;
+#pragma unroll
+  for (int r = 0; r < T::MAXRB; ++r) {
+    if (r >= nblk) continue;
+    const int local = pbk[r] * 16 + n;
+    const bool valid = local < t.q_rows && t.q_begin + local < p.total_q;
+    const int off = valid ? int((int64_t(local) * p.o_st + int64_t(head[r]) * p.o_sh) * 2) + 16 * g : 0x7ffffff0;
+#pragma unroll
+    for (int q = 0; q < D / 32; ++q) {
+      const lds_t* src = ob + r * OB + q * 4 * kOutBlk + rcol;
+      const s16x4_t a = lds_read_tr16(src), c = lds_read_tr16(src + 128);
+      __builtin_amdgcn_raw_buffer_store_b128(
+          __builtin_bit_cast(u32x4_t, (s16x8_t){a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]}), ro, off, 64 * q, 0);
     }
   }
 }
