@@ -47,8 +47,12 @@ the figures the reference's 1,532 tok/s at 32 concurrent is quoted as.
 as repeated launches captured in one hipGraph and replayed between HIP events: the ragged
 causal prefill attention of the 32 prompts for one layer (MFMA bound:
 flops = sum_b 4 * H_q * D * L_b (L_b + 1) / 2, against 2.5 PFLOP/s bf16), the
-decode-step fused RoPE + KV append (into a copy of layer 0's pool) and the
-sampler for the 32 rows (latency bound: microseconds).
+decode-step fused RoPE + KV append (into a copy of layer 0's pool), the
+prefill-sized appends of the prompts' rows into their pages (HBM bound against
+8 TB/s; fused RoPE + append bytes = 2 * T * (H_q + 2 H_kv) * D * 2 B (q, k, v
+read and written) + 2 * T * D * 2 B (cos / sin rows) + index ints; plain
+append bytes = 2 * 2 * T * H_kv * D * 2 B + index ints) and the sampler for
+the 32 rows (latency bound: microseconds).
 """
 
 from __future__ import annotations
@@ -137,6 +141,28 @@ def path_kernel_times(sch, cfg, reqs, lens, dev) -> dict:
                                                     sch.d_batch[:B], sch.d_pos[:B], pool_copy,
                                                     sch.d_indices, sch.d_indptr[: B + 1], sch.d_last[:B]), 200)
     res["rope_append_decode"] = {"us": round(us, 2), "rows": B}
+    # prefill-sized appends (HBM bound): the prompts' rows into their own pages, as the ragged
+    # prefill writes them -- fused RoPE + append of the qkv rows, and the plain K / V append
+    from minimal_inference_amd.page import append_paged_kv_cache
+
+    p_batch = torch.cat([torch.full((n,), b, dtype=torch.int32) for b, n in enumerate(lens)]).to(dev)
+    p_pos = torch.cat([torch.arange(n, dtype=torch.int32) for n in lens]).to(dev)
+    p_qkv = torch.randn(total, (hq + 2 * hkv) * d, device=dev, dtype=torch.bfloat16)
+    p_q = torch.empty(total, hq, d, device=dev, dtype=torch.bfloat16)
+    ints = 4 * ((B + 1) + int(p_indices.numel()) + B)
+    nbytes = 2 * total * (hq + 2 * hkv) * d * 2 + 2 * total * d * 2 + 4 * 3 * total + ints
+    us = time_us(lambda: rope_append_paged_kv_cache(p_qkv, hq, hkv, p_pos, model.cos, model.sin, p_batch, p_pos,
+                                                    pool_copy, p_indices, p_indptr, p_last, q_out=p_q), 20)
+    res["rope_append_prefill"] = {"us": round(us, 2), "rows": total, "mb": round(nbytes / 1e6, 1),
+                                  "gbps": round(nbytes / us / 1e3, 1),
+                                  "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBPS, 4)}
+    p_k = p_qkv[:, hq * d:(hq + hkv) * d].contiguous().view(total, hkv, d)
+    p_v = p_qkv[:, (hq + hkv) * d:].contiguous().view(total, hkv, d)
+    nbytes = 2 * 2 * total * hkv * d * 2 + 4 * 2 * total + ints
+    us = time_us(lambda: append_paged_kv_cache(p_k, p_v, p_batch, p_pos, pool_copy, p_indices, p_indptr, p_last), 20)
+    res["append_prefill"] = {"us": round(us, 2), "rows": total, "mb": round(nbytes / 1e6, 1),
+                             "gbps": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBPS, 4)}
+    del p_qkv, p_q, p_k, p_v
     # sampler: the batch's settings (half greedy, half T=0.7 / top-p 0.9)
     logits = torch.randn(B, cfg.vocab_size, device=dev, dtype=torch.float32).to(torch.bfloat16)
     smp = sch.sampler

@@ -4,9 +4,13 @@
 // NHD pool layout scheduler.py:195-202.  Slot placement is integer-exact:
 // page = kv_indices[kv_indptr[b] + pos / page_size], slot = pos % page_size.
 //
-// Each thread moves one 16-byte chunk (8 bf16) of K and the same chunk of V,
-// so a wave writes 1 KiB of contiguous head rows per instruction and the
-// kernel streams at HBM rate for prefill-sized appends.
+// One workgroup per token (grid-stride over tokens): the token's slot is a
+// chain of wave-uniform scalar loads (batch index and position, the
+// request's page-list start, the page id) done once per token, then each
+// thread moves 16-byte chunks (8 bf16) of K and the same chunks of V, so a
+// wave writes 1 KiB of contiguous head rows per instruction.
+#include <algorithm>
+
 #include "mi_common.h"
 
 namespace {
@@ -25,32 +29,48 @@ struct AppendParams {
   int32_t batch_size, num_kv_heads, head_dim, page_size;
 };
 
+typedef __attribute__((address_space(4))) const int32_t const_i32;
+
+// Base of token i's slot row in the pool (null: the token is not placed --
+// bad batch index or position, slot outside request b's page list, or a page
+// id outside the pool).  The index arrays are read through the constant
+// address space: with a wave-uniform token index the loads are scalar.
+__device__ __forceinline__ uint16_t* token_slot(const int32_t* batch_indices, const int32_t* positions,
+                                                const int32_t* indptr, const int32_t* indices, int64_t i,
+                                                int batch_size, int64_t num_pages, int page_size, uint16_t* pool,
+                                                int64_t page_stride, int64_t tok_stride) {
+  const const_i32* bi = (const const_i32*)batch_indices;
+  const const_i32* ps = (const const_i32*)positions;
+  const const_i32* ip = (const const_i32*)indptr;
+  const const_i32* ix = (const const_i32*)indices;
+  const int b = bi[i];
+  const int pos = ps[i];
+  if (b < 0 || b >= batch_size || pos < 0) return nullptr;
+  const int64_t it = int64_t(ip[b]) + pos / page_size;
+  if (it >= ip[b + 1]) return nullptr;
+  const int64_t page = ix[it];
+  if (page < 0 || page >= num_pages) return nullptr;
+  return pool + page * page_stride + int64_t(pos % page_size) * tok_stride;
+}
+
 __global__ __launch_bounds__(256) void append_kernel(AppendParams p) {
   const int chunks = p.head_dim >> 3;
-  const int64_t per_token = int64_t(p.num_kv_heads) * chunks;
-  const int64_t total = p.num_tokens * per_token;
+  const int per_token = p.num_kv_heads * chunks;
   const int64_t tok_stride = int64_t(p.num_kv_heads) * p.head_dim;
   const int64_t kv_stride = int64_t(p.page_size) * tok_stride;
   const int64_t page_stride = 2 * kv_stride;
-  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
-       idx += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t i = idx / per_token;
-    const int r = int(idx - i * per_token);
-    const int h = r / chunks;
-    const int c = r - h * chunks;
-    const int b = p.batch_indices[i];
-    const int pos = p.positions[i];
-    if (b < 0 || b >= p.batch_size || pos < 0) continue;
-    const int64_t it = int64_t(p.indptr[b]) + pos / p.page_size;
-    if (it >= p.indptr[b + 1]) continue;
-    const int64_t page = p.indices[it];
-    if (page < 0 || page >= p.num_pages) continue;
-    const int slot = pos % p.page_size;
-    uint16_t* dst = p.pool + page * page_stride + slot * tok_stride + int64_t(h) * p.head_dim + c * 8;
-    const uint4 kv = mi::load16(p.key + i * p.ks_tok + h * p.ks_head + c * 8);
-    const uint4 vv = mi::load16(p.value + i * p.vs_tok + h * p.vs_head + c * 8);
-    mi::store16(dst, kv);
-    mi::store16(dst + kv_stride, vv);
+  for (int64_t i = blockIdx.x; i < p.num_tokens; i += gridDim.x) {
+    uint16_t* slot = token_slot(p.batch_indices, p.positions, p.indptr, p.indices, i, p.batch_size, p.num_pages,
+                                p.page_size, p.pool, page_stride, tok_stride);
+    if (!slot) continue;
+    for (int u = threadIdx.x; u < per_token; u += blockDim.x) {
+      const int h = u / chunks;
+      const int c = (u - h * chunks) * 8;
+      const uint4 kv = mi::load16(p.key + i * p.ks_tok + h * p.ks_head + c);
+      const uint4 vv = mi::load16(p.value + i * p.vs_tok + h * p.vs_head + c);
+      mi::store16(slot + h * p.head_dim + c, kv);
+      mi::store16(slot + kv_stride + h * p.head_dim + c, vv);
+    }
   }
 }
 
@@ -89,13 +109,13 @@ struct RopeAppendParams {
   int32_t batch_size, num_qo_heads, num_kv_heads, head_dim, page_size;
 };
 
-// bf16(a * b) with the product exact in fp32 (8-bit x 8-bit mantissas).
-__device__ __forceinline__ float bf16_mul(float a, float b) { return mi::bf16_to_f32(mi::f32_to_bf16(a * b)); }
-
 __device__ __forceinline__ float lo16(uint32_t w) { return mi::bf16_lo(w); }
 __device__ __forceinline__ float hi16(uint32_t w) { return mi::bf16_hi(w); }
 
-// out_lo = x1 * c1 + (-x2) * s1, out_hi = x2 * c2 + x1 * s2, 8 lanes each
+// out_lo = x1 * c1 + (-x2) * s1, out_hi = x2 * c2 + x1 * s2, 8 lanes each:
+// each product is exact in fp32 (8-bit x 8-bit mantissas) and rounded to
+// bf16, the sum is taken in fp32 and rounded to bf16 (round to nearest even,
+// two values per v_cvt_pk_bf16_f32)
 __device__ __forceinline__ void rope8(uint4 x1, uint4 x2, uint4 c1, uint4 s1, uint4 c2, uint4 s2, uint4& o1,
                                       uint4& o2) {
   const uint32_t* a = &x1.x;
@@ -108,66 +128,60 @@ __device__ __forceinline__ void rope8(uint4 x1, uint4 x2, uint4 c1, uint4 s1, ui
   uint32_t* ob = &o2.x;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    float r0, r1;
-    r0 = bf16_mul(lo16(a[w]), lo16(ca[w])) + bf16_mul(-lo16(b[w]), lo16(sa[w]));
-    r1 = bf16_mul(hi16(a[w]), hi16(ca[w])) + bf16_mul(-hi16(b[w]), hi16(sa[w]));
-    oa[w] = mi::pack_bf16x2(r0, r1);
-    r0 = bf16_mul(lo16(b[w]), lo16(cb[w])) + bf16_mul(lo16(a[w]), lo16(sb[w]));
-    r1 = bf16_mul(hi16(b[w]), hi16(cb[w])) + bf16_mul(hi16(a[w]), hi16(sb[w]));
-    ob[w] = mi::pack_bf16x2(r0, r1);
+    const uint32_t ac = mi::cvt_pk_bf16(lo16(a[w]) * lo16(ca[w]), hi16(a[w]) * hi16(ca[w]));
+    const uint32_t bs = mi::cvt_pk_bf16(-lo16(b[w]) * lo16(sa[w]), -hi16(b[w]) * hi16(sa[w]));
+    oa[w] = mi::cvt_pk_bf16(lo16(ac) + lo16(bs), hi16(ac) + hi16(bs));
+    const uint32_t bc = mi::cvt_pk_bf16(lo16(b[w]) * lo16(cb[w]), hi16(b[w]) * hi16(cb[w]));
+    const uint32_t as = mi::cvt_pk_bf16(lo16(a[w]) * lo16(sb[w]), hi16(a[w]) * hi16(sb[w]));
+    ob[w] = mi::cvt_pk_bf16(lo16(bc) + lo16(as), hi16(bc) + hi16(as));
   }
 }
 
+// One workgroup per token (grid-stride over tokens): slot and RoPE row are
+// looked up once per token with scalar loads; the threads cover the token's
+// rotate units and V chunks.
 __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams p) {
   const int d = p.head_dim, half = d >> 1;
-  const int rot_units = (p.num_qo_heads + p.num_kv_heads) * (d >> 4);
+  const int upr = d >> 4;  // rotate units per head
+  const int rot_units = (p.num_qo_heads + p.num_kv_heads) * upr;
   const int per_token = rot_units + p.num_kv_heads * (d >> 3);
-  const int64_t total = p.num_tokens * per_token;
   const int64_t tok_stride = int64_t(p.num_kv_heads) * d;
   const int64_t kv_stride = int64_t(p.page_size) * tok_stride;
   const int64_t page_stride = 2 * kv_stride;
-  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
-       idx += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t i = idx / per_token;
-    const int r = int(idx - i * per_token);
+  const const_i32* rope_pos = (const const_i32*)p.rope_pos;
+  for (int64_t i = blockIdx.x; i < p.num_tokens; i += gridDim.x) {
+    // null: K / V of the token are not placed (q is still rotated)
+    uint16_t* slot = token_slot(p.batch_indices, p.positions, p.indptr, p.indices, i, p.batch_size, p.num_pages,
+                                p.page_size, p.pool, page_stride, tok_stride);
+    int rp = rope_pos[i];
+    rp = rp < 0 ? 0 : (rp >= p.table_rows ? int(p.table_rows - 1) : rp);
+    const uint16_t* cs = p.cos + int64_t(rp) * d;
+    const uint16_t* sn = p.sin + int64_t(rp) * d;
     const uint16_t* row = p.qkv + i * p.qkv_stride;
-    // page slot of token i (K and V units only)
-    auto slot_ptr = [&](int kh) -> uint16_t* {
-      const int b = p.batch_indices[i];
-      const int pos = p.positions[i];
-      if (b < 0 || b >= p.batch_size || pos < 0) return nullptr;
-      const int64_t it = int64_t(p.indptr[b]) + pos / p.page_size;
-      if (it >= p.indptr[b + 1]) return nullptr;
-      const int64_t page = p.indices[it];
-      if (page < 0 || page >= p.num_pages) return nullptr;
-      return p.pool + page * page_stride + (pos % p.page_size) * tok_stride + int64_t(kh) * d;
-    };
-    if (r < rot_units) {
-      const int h = r / (d >> 4);
-      const int c = (r - h * (d >> 4)) * 8;
-      int rp = p.rope_pos[i];
-      rp = rp < 0 ? 0 : (rp >= p.table_rows ? int(p.table_rows - 1) : rp);
-      const uint16_t* cs = p.cos + int64_t(rp) * d;
-      const uint16_t* sn = p.sin + int64_t(rp) * d;
-      const uint16_t* src = row + int64_t(h) * d;
-      uint4 o1, o2;
-      rope8(mi::load16(src + c), mi::load16(src + half + c), mi::load16(cs + c), mi::load16(sn + c),
-            mi::load16(cs + half + c), mi::load16(sn + half + c), o1, o2);
-      if (h < p.num_qo_heads) {
-        uint16_t* dst = p.q_out + i * p.qo_stride_tok + int64_t(h) * p.qo_stride_head;
-        mi::store16(dst + c, o1);
-        mi::store16(dst + half + c, o2);
-      } else if (uint16_t* dst = slot_ptr(h - p.num_qo_heads)) {
-        mi::store16(dst + c, o1);
-        mi::store16(dst + half + c, o2);
-      }
-    } else {
-      const int u = r - rot_units;
-      const int kh = u / (d >> 3);
-      const int c = (u - kh * (d >> 3)) * 8;
-      if (uint16_t* dst = slot_ptr(kh))
-        mi::store16(dst + kv_stride + c,
+    for (int u = threadIdx.x; u < per_token; u += blockDim.x) {
+      if (u < rot_units) {
+        const int h = u / upr;
+        const int c = (u - h * upr) * 8;
+        const uint16_t* src = row + int64_t(h) * d;
+        uint4 o1, o2;
+        rope8(mi::load16(src + c), mi::load16(src + half + c), mi::load16(cs + c), mi::load16(sn + c),
+              mi::load16(cs + half + c), mi::load16(sn + half + c), o1, o2);
+        if (h < p.num_qo_heads) {
+          uint16_t* dst = p.q_out + i * p.qo_stride_tok + int64_t(h) * p.qo_stride_head;
+          mi::store16(dst + c, o1);
+          mi::store16(dst + half + c, o2);
+        } else if (slot) {
+          uint16_t* dst = slot + int64_t(h - p.num_qo_heads) * d;
+          mi::store16(dst + c, o1);
+          mi::store16(dst + half + c, o2);
+        }
+      } else if (slot) {
+        const int v = u - rot_units;
+        const int kh = v / (d >> 3);
+        const int c = (v - kh * (d >> 3)) * 8;
+        mi::store16(slot + kv_stride + int64_t(kh) * d + c,
                     mi::load16(row + int64_t(p.num_qo_heads + p.num_kv_heads + kh) * d + c));
+      }
     }
   }
 }
@@ -218,11 +232,10 @@ extern "C" int mi_paged_kv_append(const void* append_key, int64_t key_stride_tok
                  num_kv_heads,
                  head_dim,
                  page_size};
-  const int64_t work = num_tokens * num_kv_heads * (head_dim / 8);
-  const int threads = 256;
-  int64_t blocks = (work + threads - 1) / threads;
-  const int64_t cap = int64_t(mi::num_cus()) * 16;
-  if (blocks > cap) blocks = cap;
+  // one workgroup per token, up to 256 threads over its chunks
+  const int64_t per_token = int64_t(num_kv_heads) * (head_dim / 8);
+  const int threads = int(std::min<int64_t>(256, (per_token + 63) / 64 * 64));
+  const int64_t blocks = std::min<int64_t>(num_tokens, int64_t(1) << 20);
   hipLaunchKernelGGL(append_kernel, dim3(unsigned(blocks)), dim3(threads), 0,
                      static_cast<hipStream_t>(stream), p);
   return mi::check_launch("append_kernel");
@@ -278,11 +291,9 @@ extern "C" int mi_rope_append(const void* qkv, int64_t qkv_stride_token, const i
                      head_dim,
                      page_size};
   const int64_t per_token = int64_t(num_qo_heads + num_kv_heads) * (head_dim / 16) + int64_t(num_kv_heads) * (head_dim / 8);
-  const int64_t work = num_tokens * per_token;
-  const int threads = 256;
-  int64_t blocks = (work + threads - 1) / threads;
-  const int64_t cap = int64_t(mi::num_cus()) * 16;
-  if (blocks > cap) blocks = cap;
+  // one workgroup per token, up to 256 threads over its units
+  const int threads = int(std::min<int64_t>(256, (per_token + 63) / 64 * 64));
+  const int64_t blocks = std::min<int64_t>(num_tokens, int64_t(1) << 20);
   hipLaunchKernelGGL(rope_append_kernel, dim3(unsigned(blocks)), dim3(threads), 0,
                      static_cast<hipStream_t>(stream), p);
   return mi::check_launch("rope_append_kernel");
