@@ -16,12 +16,14 @@
 //              rounded to bf16 as torch's bf16 silu is, then the bf16 product.
 #include <math.h>
 
+#include <algorithm>
+
 #include "mi_common.h"
 
 namespace {
 
-constexpr int kNormThreads = 256;
-constexpr int kMaxChunks = 8;  // 16-byte chunks per thread: hidden <= 256 * 8 * 8 = 16384
+constexpr int kNormMaxThreads = 1024;
+constexpr int kMaxChunks = 2;  // 16-byte chunks per thread: hidden <= 1024 * 2 * 8 = 16384
 
 struct AddRmsParams {
   const uint16_t* x;
@@ -40,60 +42,65 @@ struct AddRmsParams {
 __device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ void st16(uint16_t* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
 
-// One workgroup per row; the row stays in registers between the two passes.
-__global__ __launch_bounds__(kNormThreads) void add_rms_kernel(AddRmsParams p) {
-  __shared__ float red[kNormThreads / 64];
+// One workgroup per row, one or two 16-byte chunks per thread (up to 1,024
+// threads): every load of the row -- x, delta and the norm weight -- is
+// issued before anything is computed or stored (x may be written in place),
+// so a row costs one memory round trip; the row stays in registers between
+// the sum and the normalisation.
+__global__ __launch_bounds__(kNormMaxThreads) void add_rms_kernel(AddRmsParams p) {
+  __shared__ float red[kNormMaxThreads / 64];
   const int64_t row = blockIdx.x;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, nt = blockDim.x;
   const int nch = p.hidden / 8;
   const uint16_t* x = p.x + row * p.x_stride;
+  uint4 xv[kMaxChunks], dv[kMaxChunks], wv[kMaxChunks];
+#pragma unroll
+  for (int c = 0; c < kMaxChunks; ++c) {
+    const int ch = tid + c * nt;
+    xv[c] = dv[c] = wv[c] = make_uint4(0u, 0u, 0u, 0u);
+    if (ch < nch) {
+      xv[c] = ld16(x + ch * 8);
+      if (p.delta) dv[c] = ld16(p.delta + row * p.d_stride + ch * 8);
+      if (p.h_out) wv[c] = ld16(p.weight + ch * 8);
+    }
+  }
   float v[kMaxChunks][8];
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < kMaxChunks; ++c) {
-    const int ch = tid + c * kNormThreads;
-    if (ch >= nch) break;
-    const uint4 xv = ld16(x + ch * 8);
-    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-    uint32_t dw[4] = {0, 0, 0, 0};
-    if (p.delta) {
-      const uint4 dv = ld16(p.delta + row * p.d_stride + ch * 8);
-      dw[0] = dv.x, dw[1] = dv.y, dw[2] = dv.z, dw[3] = dv.w;
-    }
+    const int ch = tid + c * nt;
+    const uint32_t xw[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+    const uint32_t dw[4] = {dv[c].x, dv[c].y, dv[c].z, dv[c].w};
     uint32_t ow[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      float a = mi::bf16_lo(xw[k]), b = mi::bf16_hi(xw[k]);
-      if (p.delta) {
-        a = mi::bf16_to_f32(mi::f32_to_bf16(a + mi::bf16_lo(dw[k])));
-        b = mi::bf16_to_f32(mi::f32_to_bf16(b + mi::bf16_hi(dw[k])));
-      }
+      // the bf16 add: fp32 sum rounded to bf16 (zeros past the row add nothing)
+      ow[k] = p.delta ? mi::cvt_pk_bf16(mi::bf16_lo(xw[k]) + mi::bf16_lo(dw[k]), mi::bf16_hi(xw[k]) + mi::bf16_hi(dw[k]))
+                      : xw[k];
+      const float a = mi::bf16_lo(ow[k]), b = mi::bf16_hi(ow[k]);
       v[c][2 * k] = a;
       v[c][2 * k + 1] = b;
       ss = fmaf(a, a, ss);
       ss = fmaf(b, b, ss);
-      ow[k] = mi::pack_bf16x2(a, b);
     }
-    if (p.x_out) st16(p.x_out + row * p.xo_stride + ch * 8, make_uint4(ow[0], ow[1], ow[2], ow[3]));
+    if (p.x_out && ch < nch) st16(p.x_out + row * p.xo_stride + ch * 8, make_uint4(ow[0], ow[1], ow[2], ow[3]));
   }
   if (!p.h_out) return;
   ss = mi::wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
   float tot = 0.f;
-#pragma unroll
-  for (int w = 0; w < kNormThreads / 64; ++w) tot += red[w];
+  for (int w = 0; w < nt / 64; ++w) tot += red[w];
   const float rstd = rsqrtf(tot / float(p.hidden) + p.eps);
 #pragma unroll
   for (int c = 0; c < kMaxChunks; ++c) {
-    const int ch = tid + c * kNormThreads;
+    const int ch = tid + c * nt;
     if (ch >= nch) break;
-    const uint4 wv = ld16(p.weight + ch * 8);
-    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    const uint32_t ww[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
     uint32_t hw[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-      hw[k] = mi::pack_bf16x2(v[c][2 * k] * rstd * mi::bf16_lo(ww[k]), v[c][2 * k + 1] * rstd * mi::bf16_hi(ww[k]));
+      hw[k] = mi::cvt_pk_bf16(v[c][2 * k] * rstd * mi::bf16_lo(ww[k]), v[c][2 * k + 1] * rstd * mi::bf16_hi(ww[k]));
     st16(p.h_out + row * p.h_stride + ch * 8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
   }
 }
@@ -137,9 +144,9 @@ extern "C" int mi_add_rms_norm(const void* x, int64_t x_stride, const void* delt
                                const void* weight, void* x_out, int64_t x_out_stride, void* h_out,
                                int64_t h_stride, int64_t rows, int32_t hidden, float eps, mi_stream_t stream) {
   mi::clear_error();
-  if (rows < 0 || hidden <= 0 || hidden % 8 || hidden > kNormThreads * kMaxChunks * 8)
+  if (rows < 0 || hidden <= 0 || hidden % 8 || hidden > kNormMaxThreads * kMaxChunks * 8)
     return mi::fail(MI_ERR_INVALID, "add_rms_norm: hidden %d (multiple of 8, <= %d)", hidden,
-                    kNormThreads * kMaxChunks * 8);
+                    kNormMaxThreads * kMaxChunks * 8);
   if (rows == 0) return MI_OK;
   if (!x || (h_out && !weight) || (!h_out && !x_out))
     return mi::fail(MI_ERR_INVALID, "add_rms_norm: null pointer argument");
@@ -160,7 +167,10 @@ extern "C" int mi_add_rms_norm(const void* x, int64_t x_stride, const void* delt
   p.h_stride = h_stride;
   p.hidden = hidden;
   p.eps = eps;
-  hipLaunchKernelGGL(add_rms_kernel, dim3(uint32_t(rows)), dim3(kNormThreads), 0, static_cast<hipStream_t>(stream), p);
+  // a thread per 16-byte chunk up to 1,024 threads, two chunks each beyond
+  const int nch = hidden / 8;
+  const int threads = std::min(kNormMaxThreads, (nch + 63) / 64 * 64);
+  hipLaunchKernelGGL(add_rms_kernel, dim3(uint32_t(rows)), dim3(threads), 0, static_cast<hipStream_t>(stream), p);
   return mi::check_launch("add_rms_kernel");
 }
 
