@@ -11,7 +11,7 @@ of the device page table and the HIP kernels:
   (984-1003); released pages are zeroed in every layer (216-221);
 * greedy rows (temperature <= 0) take argmax, others sample (319-343).
 
-What changes (the north star's items):
+What changes relative to the reference:
 * page lists, the free-page ring and the CSR / padding metadata live on the
   GPU (``DevicePageTable``); the host keeps counts only;
 * all requests admitted in a step are prefilled in one ragged batch (the
