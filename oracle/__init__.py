@@ -3,7 +3,7 @@
 This package restates, on the CPU, the arithmetic of the reference's
 paged-attention hot path so that the HIP kernels can be checked against it.
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import it, and only as the checker (or the timed CPU
+``bench.py`` may import it, and only to check results (or as the timed CPU
 baseline); the product package never imports it and has no CPU fallback.
 
 Modules:
