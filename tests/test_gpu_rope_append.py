@@ -50,7 +50,7 @@ def _run(dev, qkv_full, width, hq, hkv, rope_pos, cos, sin, bi, pos, pool, indic
 
 
 @pytest.mark.parametrize("hq,hkv,d,theta", [(32, 8, 128, 1e6), (14, 2, 64, 1e6), (28, 4, 128, 1e6),
-                                            (8, 8, 256, 1e4), (12, 4, 64, 1e4)])
+                                            (64, 8, 128, 1e6), (8, 8, 256, 1e4), (12, 4, 64, 1e4)])
 @pytest.mark.parametrize("separate_q", [False, True])
 def test_decode_rows_bit_exact(dev, hq, hkv, d, theta, separate_q):
     lens = [17, 64, 203, 511, 1, 16, 900]
