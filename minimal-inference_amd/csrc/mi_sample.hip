@@ -82,38 +82,68 @@ __device__ __forceinline__ void betterf(float& bv, int& bi, float v, int i) {
   }
 }
 
+// (value, index) argmax across lanes without LDS: each step fetches a
+// partner's pair with a DPP or lane-swap move and keeps the better one.
 template <typename F>
-__device__ __forceinline__ void block_argmax(F& bv, int& bi, F* sv, int* si) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (int o = 32; o > 0; o >>= 1) {
-    F ov;
-    if constexpr (sizeof(F) == 4 && (F(0.5) != F(0))) {
-      ov = __shfl_xor(bv, o);
-    } else {
-      ov = F(__shfl_xor(int(bv), o));
-    }
-    const int oi = __shfl_xor(bi, o);
-    if (ov > bv || (ov == bv && oi < bi)) {
-      bv = ov;
-      bi = oi;
-    }
+__device__ __forceinline__ void arg_take(F& bv, int& bi, uint32_t ov_bits, int oi) {
+  const F ov = __builtin_bit_cast(F, ov_bits);
+  if (ov > bv || (ov == bv && oi < bi)) {
+    bv = ov;
+    bi = oi;
   }
-  __syncthreads();
+}
+template <int CTRL, typename F>
+__device__ __forceinline__ void arg_dpp(F& bv, int& bi) {
+  const uint32_t ov = uint32_t(__builtin_amdgcn_update_dpp(0, int(__builtin_bit_cast(uint32_t, bv)), CTRL, 0xf, 0xf, false));
+  const int oi = __builtin_amdgcn_update_dpp(0, bi, CTRL, 0xf, 0xf, false);
+  arg_take(bv, bi, ov, oi);
+}
+// Every lane of each aligned group of 16 ends with the group's best pair.
+template <typename F>
+__device__ __forceinline__ void group16_argmax(F& bv, int& bi) {
+  arg_dpp<mi::kDppQuadSwap1>(bv, bi);
+  arg_dpp<mi::kDppQuadSwap2>(bv, bi);
+  arg_dpp<mi::kDppRowHalfMirror>(bv, bi);
+  arg_dpp<mi::kDppRowMirror>(bv, bi);
+}
+// The swaps exchange values between lane halves; both results are taken
+// (one of them is the lane's own pair, which changes nothing).
+template <typename F>
+__device__ __forceinline__ void wave_argmax(F& bv, int& bi) {
+  group16_argmax(bv, bi);
+  {
+    const uint32_t v = __builtin_bit_cast(uint32_t, bv);
+    const auto rv = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    const auto ri = __builtin_amdgcn_permlane16_swap(uint32_t(bi), uint32_t(bi), false, false);
+    arg_take(bv, bi, rv[0], int(ri[0]));
+    arg_take(bv, bi, rv[1], int(ri[1]));
+  }
+  {
+    const uint32_t v = __builtin_bit_cast(uint32_t, bv);
+    const auto rv = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    const auto ri = __builtin_amdgcn_permlane32_swap(uint32_t(bi), uint32_t(bi), false, false);
+    arg_take(bv, bi, rv[0], int(ri[0]));
+    arg_take(bv, bi, rv[1], int(ri[1]));
+  }
+}
+
+// Workgroup argmax (larger value, then lower index); every thread gets the
+// result.  `lowest` ranks below every candidate.  sv / si hold one pair per
+// wave; the call starts and ends with them free.
+template <typename F>
+__device__ __forceinline__ void block_argmax(F& bv, int& bi, F* sv, int* si, F lowest) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  wave_argmax(bv, bi);
   if (lane == 0) {
     sv[w] = bv;
     si[w] = bi;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int k = 1; k < kThreads / 64; ++k)
-      if (sv[k] > sv[0] || (sv[k] == sv[0] && si[k] < si[0])) {
-        sv[0] = sv[k];
-        si[0] = si[k];
-      }
-  }
-  __syncthreads();
-  bv = sv[0];
-  bi = si[0];
+  F v = lane < kThreads / 64 ? sv[lane] : lowest;
+  int i = lane < kThreads / 64 ? si[lane] : 0x7fffffff;
+  group16_argmax(v, i);  // the kThreads / 64 = 16 pairs sit in lanes 0..15
+  bv = __builtin_bit_cast(F, uint32_t(__builtin_amdgcn_readfirstlane(int(__builtin_bit_cast(uint32_t, v)))));
+  bi = __builtin_amdgcn_readfirstlane(i);
   __syncthreads();
 }
 
@@ -139,7 +169,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams p) {
     uint32_t bk = 0;
     int bi = 0x7fffffff;
     for (int i = tid; i < V; i += kThreads) better(bk, bi, bf16_key(x[i]), i);
-    block_argmax<uint32_t>(bk, bi, sh_u, sh_i);
+    block_argmax<uint32_t>(bk, bi, sh_u, sh_i, 0u);
     if (tid == 0) p.out[row] = bi < V ? bi : 0;
     return;
   }
@@ -154,7 +184,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams p) {
   {
     int unused = 0;
     for (int i = tid; i < V; i += kThreads) better(mk, unused, bf16_key(scaled(i)), 0);
-    block_argmax<uint32_t>(mk, unused, sh_u, sh_i);
+    block_argmax<uint32_t>(mk, unused, sh_u, sh_i, 0u);
   }
   const float smax = key_to_f32(mk) * mi::kLog2e;
 
@@ -239,7 +269,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams p) {
       betterf(bv, bi, v, i);
     }
   }
-  block_argmax<float>(bv, bi, sh_f, sh_i);
+  block_argmax<float>(bv, bi, sh_f, sh_i, -INFINITY);
   if (tid == 0) p.out[row] = bi < V ? bi : 0;
 }
 
@@ -322,13 +352,13 @@ __global__ __launch_bounds__(kThreads) void sample_cached_kernel(SampleParams p)
   }
 
   if (greedy) {
-    block_argmax<uint32_t>(bk, bi, sh_u, sh_i);
+    block_argmax<uint32_t>(bk, bi, sh_u, sh_i, 0u);
     if (tid == 0) p.out[row] = bi < V ? bi : 0;
     return;
   }
   {
     int unused = 0;
-    block_argmax<uint32_t>(mk, unused, sh_u, sh_i);  // ends with barriers: keys[] is complete
+    block_argmax<uint32_t>(mk, unused, sh_u, sh_i, 0u);  // ends with barriers: keys[] is complete
   }
   const float smax = key_to_f32(mk) * mi::kLog2e;
 
@@ -428,7 +458,7 @@ __global__ __launch_bounds__(kThreads) void sample_cached_kernel(SampleParams p)
       betterf(bv, bi, v, i);
     }
   }
-  block_argmax<float>(bv, bi, sh_f, sh_i);
+  block_argmax<float>(bv, bi, sh_f, sh_i, -INFINITY);
   if (tid == 0) p.out[row] = bi < V ? bi : 0;
 }
 
