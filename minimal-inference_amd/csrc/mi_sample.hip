@@ -177,7 +177,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams p) {
   // clamp(min=1e-6) in bf16, then s_i = bf16(logit_i / t)
   const float tmin = mi::bf16_to_f32(mi::f32_to_bf16(1e-6f));
   const float tc = fmaxf(tq, tmin);
-  auto scaled = [&](int i) -> uint16_t { return mi::f32_to_bf16(mi::bf16_to_f32(x[i]) / tc); };
+  auto scaled = [&](int i) -> uint16_t { return mi::cvt_bf16(mi::bf16_to_f32(x[i]) / tc); };
 
   // ---- max key
   uint32_t mk = 0;
@@ -343,7 +343,8 @@ __global__ __launch_bounds__(kThreads) void sample_cached_kernel(SampleParams p)
     uint32_t k[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const uint16_t sv = greedy ? v[e] : mi::f32_to_bf16(mi::bf16_to_f32(v[e]) / tc);
+      // bf16(x / t): the fp32 quotient rounded to nearest even by v_cvt_pk_bf16_f32
+      const uint16_t sv = greedy ? v[e] : mi::cvt_bf16(mi::bf16_to_f32(v[e]) / tc);
       k[e] = (t0 + e < V) ? key16(sv) : 0u;
       if (t0 + e < V) better(bk, bi, k[e], t0 + e);
       mk = max(mk, k[e]);
