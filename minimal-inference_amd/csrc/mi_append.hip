@@ -144,6 +144,9 @@ __device__ __forceinline__ void rope8(uint4 x1, uint4 x2, uint4 c1, uint4 s1, ui
 // One workgroup per token (grid-stride over tokens): the RoPE row and the
 // slot are looked up once per token with scalar loads; the threads rotate
 // the q heads first, then the k heads and copy the V chunks into the slot.
+// The qkv rows are read once and loaded non-temporal (80 -> 71 us on 18,240
+// rows of 32 / 8 heads; the same loads made the plain append slower, 26 ->
+// 29 us, so append_kernel keeps ordinary loads).
 __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams p) {
   const int d = p.head_dim, half = d >> 1;
   const int upr = d >> 4;  // rotate units per head
@@ -165,7 +168,7 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams p) {
       const int c = (u - h * upr) * 8;
       const uint16_t* src = row + int64_t(h) * d;
       uint4 o1, o2;
-      rope8(mi::load16(src + c), mi::load16(src + half + c), mi::load16(cs + c), mi::load16(sn + c),
+      rope8(mi::load16_nt(src + c), mi::load16_nt(src + half + c), mi::load16(cs + c), mi::load16(sn + c),
             mi::load16(cs + half + c), mi::load16(sn + half + c), o1, o2);
       uint16_t* dst = p.q_out + i * p.qo_stride_tok + int64_t(h) * p.qo_stride_head;
       mi::store16(dst + c, o1);
@@ -183,7 +186,7 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams p) {
         const int c = (u - h * upr) * 8;
         const uint16_t* src = row + int64_t(h) * d;
         uint4 o1, o2;
-        rope8(mi::load16(src + c), mi::load16(src + half + c), mi::load16(cs + c), mi::load16(sn + c),
+        rope8(mi::load16_nt(src + c), mi::load16_nt(src + half + c), mi::load16(cs + c), mi::load16(sn + c),
               mi::load16(cs + half + c), mi::load16(sn + half + c), o1, o2);
         uint16_t* dst = slot + int64_t(h - p.num_qo_heads) * d;
         mi::store16(dst + c, o1);
@@ -193,7 +196,7 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams p) {
         const int kh = v / (d >> 3);
         const int c = (v - kh * (d >> 3)) * 8;
         mi::store16(slot + kv_stride + int64_t(kh) * d + c,
-                    mi::load16(row + int64_t(p.num_qo_heads + p.num_kv_heads + kh) * d + c));
+                    mi::load16_nt(row + int64_t(p.num_qo_heads + p.num_kv_heads + kh) * d + c));
       }
     }
   }

@@ -119,6 +119,13 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 __device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+// A 16-byte load marked non-temporal (nt): for rows read once, so they do not
+// push reused data out of L2.
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_nt_t;
+__device__ __forceinline__ uint4 load16_nt(const void* p) {
+  const u32x4_nt_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt_t*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
 __device__ __forceinline__ void store16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
 
 constexpr float kLog2e = 1.4426950408889634f;
