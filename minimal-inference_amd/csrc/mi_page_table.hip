@@ -192,7 +192,8 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
   if (t == 0) s_indptr[0] = 0;
   __syncthreads();
   const int tot_pages = s_indptr[padded];
-  if (t <= padded) p.indptr[t] = s_indptr[t];
+  // padded + 1 entries: with padded == kThreads the last one has no thread of its own
+  for (int i = t; i <= padded; i += kThreads) p.indptr[i] = s_indptr[i];
   if (t < padded) {
     if (t < n_dec) {
       const int seq = pos_row + 1;

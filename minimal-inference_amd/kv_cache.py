@@ -172,40 +172,52 @@ class DevicePageTable:
         Released pages are zeroed by the caller via ``released`` (the count is
         returned).
         """
-        rel = [s for s, _ in self._pending_release]
-        released_pages = sum(n for _, n in self._pending_release)
-        self._pending_release = []
-        n_rel = len(rel)
-        n_adm = 0
-        for s, n in admits:
-            if n > self.free_count:
-                raise RuntimeError(f"Cannot allocate {n} pages, only {self.free_count} free")
-            if self.slot_npages[s] + n > self.mpps:
-                raise RuntimeError(f"slot {s} would exceed {self.mpps} pages")
-            self.free_count -= n
-            self.slot_npages[s] += n
-            n_adm += 1
-        grow = 0
-        for s, pos in rows:
-            need = self.pages_needed(pos + 1) - self.slot_npages[s]
-            if need > 0:
-                if self.slot_npages[s] + need > self.mpps:
-                    raise RuntimeError(f"slot {s} would exceed {self.mpps} pages")
-                grow += need
-                self.slot_npages[s] += need
-        if grow > self.free_count:
-            raise RuntimeError(f"Cannot allocate {grow} pages, only {self.free_count} free")
-        self.free_count -= grow
+        # Every check runs on prospective counts first; the host mirror (free
+        # count, pages per slot, pending releases) changes only once the
+        # step's kernel has been launched, so a step that raises leaves the
+        # mirror equal to the device state.
         if padded < len(rows) or padded > 1024:
             raise ValueError("padded batch must be in [rows, 1024]")
-        total_pages = sum(self.slot_npages[s] for s, _ in rows) + (padded - len(rows))
-        if total_pages > indices.numel():
-            raise ValueError(f"indices buffer holds {indices.numel()} ids, step needs {total_pages}")
         for name, t, n in (("indptr", indptr, padded + 1), ("last_page_len", last_page_len, padded),
                            ("batch_indices", batch_indices, padded), ("positions", positions, padded)):
             require_gpu(name, t)
             if t.dtype != torch.int32 or t.numel() < n:
                 raise ValueError(f"{name} must be int32 with >= {n} entries")
+        rel = [s for s, _ in self._pending_release]
+        released_pages = sum(n for _, n in self._pending_release)
+        n_rel = len(rel)
+        free = self.free_count
+        npages = {}  # slot -> prospective page count
+
+        def held(s: int) -> int:
+            return npages.get(s, self.slot_npages[s])
+
+        for s, n in admits:
+            if not 0 <= s < self.max_slots or n < 0:
+                raise ValueError(f"bad admission (slot {s}, {n} pages)")
+            if n > free:
+                raise RuntimeError(f"Cannot allocate {n} pages, only {free} free")
+            if held(s) + n > self.mpps:
+                raise RuntimeError(f"slot {s} would exceed {self.mpps} pages")
+            free -= n
+            npages[s] = held(s) + n
+        n_adm = len(admits)
+        grow = 0
+        for s, pos in rows:
+            if not 0 <= s < self.max_slots or pos < 0:
+                raise ValueError(f"bad decode row (slot {s}, position {pos})")
+            need = self.pages_needed(pos + 1) - held(s)
+            if need > 0:
+                if held(s) + need > self.mpps:
+                    raise RuntimeError(f"slot {s} would exceed {self.mpps} pages")
+                grow += need
+                npages[s] = held(s) + need
+        if grow > free:
+            raise RuntimeError(f"Cannot allocate {grow} pages, only {free} free")
+        free -= grow
+        total_pages = sum(held(s) for s, _ in rows) + (padded - len(rows))
+        if total_pages > indices.numel():
+            raise ValueError(f"indices buffer holds {indices.numel()} ids, step needs {total_pages}")
         ops = [n_rel, n_adm, len(rows), padded]
         ops += rel
         ops += [s for s, _ in admits]
@@ -231,4 +243,8 @@ class DevicePageTable:
             indices.numel(), last_page_len.data_ptr(), batch_indices.data_ptr(), positions.data_ptr(),
             self.released.data_ptr(), torch.cuda.current_stream(self.device).cuda_stream,
         )
+        self._pending_release = []
+        self.free_count = free
+        for s, n in npages.items():
+            self.slot_npages[s] = n
         return released_pages

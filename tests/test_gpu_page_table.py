@@ -139,3 +139,60 @@ def test_release_zeroes_pages_in_every_layer(dev):
             assert int(kv.data[:, p].abs().sum()) == 0
         else:
             assert torch.equal(kv.data[:, p], before[:, p])
+
+
+def test_padded_batch_of_1024_writes_every_indptr_entry(dev):
+    """padded == 1024 (one row per thread of the page-table kernel): the
+    1,025th indptr entry must be written too, against the oracle CSR."""
+    from minimal_inference_amd.kv_cache import DevicePageTable
+
+    n_rows, padded = 1000, 1024
+    pt = DevicePageTable(4096, n_rows, 4, 16, dev)
+    indptr = torch.full((padded + 1,), -7, dtype=torch.int32, device=dev)
+    indices = torch.full((padded * 4,), -7, dtype=torch.int32, device=dev)
+    last = torch.zeros(padded, dtype=torch.int32, device=dev)
+    bidx = torch.zeros(padded, dtype=torch.int32, device=dev)
+    pos = torch.zeros(padded, dtype=torch.int32, device=dev)
+    lens = [1 + (7 * i) % 40 for i in range(n_rows)]  # 1..40 tokens: 1..3 pages
+    admits = [(i, pt.pages_needed(n)) for i, n in enumerate(lens)]
+    pt.step(admits, [], 0, indptr, indices, last, bidx, pos)
+    rows = [(i, n - 1) for i, n in enumerate(lens)]
+    pt.step([], rows, padded, indptr, indices, last, bidx, pos)
+    npages = [pt.pages_needed(n) for n in lens] + [1] * (padded - n_rows)
+    want = [0]
+    for n in npages:
+        want.append(want[-1] + n)
+    got = indptr.cpu().tolist()
+    assert got == want
+    # real rows got consecutive ring pages in admission order, padding rows the scratch page
+    ix = indices[: want[-1]].cpu().tolist()
+    assert ix[: want[n_rows]] == list(range(want[n_rows]))
+    assert ix[want[n_rows]:] == [4095] * (padded - n_rows)
+    assert pt.error_word() == 0
+
+
+def test_failed_step_leaves_the_host_mirror_unchanged(dev):
+    """A step that raises before its launch must not move the host counts:
+    the device never saw it, so free_count / pages per slot / pending
+    releases stay as they were and the next step still matches the oracle."""
+    from minimal_inference_amd.kv_cache import DevicePageTable
+
+    pt = DevicePageTable(40, 4, 8, 16, dev)
+    buf = [torch.zeros(16, dtype=torch.int32, device=dev) for _ in range(5)]
+    pt.step([(0, 2), (1, 3)], [], 0, *buf)
+    pt.release(1)
+    before = (pt.free_count, list(pt.slot_npages), list(pt._pending_release))
+    small = torch.zeros(2, dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError):  # indices buffer too small for the step's pages
+        pt.step([(2, 5)], [(0, 40), (2, 70)], 2, buf[0], small, buf[2], buf[3], buf[4])
+    with pytest.raises(ValueError):  # padded batch below the row count
+        pt.step([(2, 1)], [(0, 20), (2, 3)], 1, *buf)
+    with pytest.raises(RuntimeError):  # admission beyond the pool
+        pt.step([(2, 9), (3, 30)], [], 0, *buf)
+    assert (pt.free_count, pt.slot_npages, pt._pending_release) == before
+    # the real step: release of slot 1 (3 pages to the ring tail), then growth of slot 0
+    pt.step([], [(0, 40)], 1, *buf)
+    assert buf[0][:2].cpu().tolist() == [0, 3]
+    assert buf[1][:3].cpu().tolist() == [0, 1, 5]
+    assert pt.free_count == 39 - 3
+    assert pt.error_word() == 0
