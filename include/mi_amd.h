@@ -128,6 +128,31 @@ int mi_decode_run(void* workspace, size_t workspace_bytes, const void* q, int64_
                   int32_t max_units, mi_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
+ * Decode attention with no caller workspace.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under graph capture that may not call hipMalloc, allocation-
+ * free serving loops).  It runs the plan and the run of mi_decode_plan /
+ * mi_decode_run (same kernels, same results) with the work list in a static
+ * device array of mi_decode_static_capacity() bytes (16 MiB; each GPU the
+ * library runs on holds one until the process ends) instead of a workspace.
+ * Arguments mean what they mean for mi_decode_plan + mi_decode_run.  A batch
+ * whose work list does not fit the array (batch x num_kv_heads beyond a few
+ * thousand units at head_dim 128) returns MI_ERR_WORKSPACE.  It allocates
+ * nothing and never frees.  All calls on one device share that device's
+ * array: calls that overlap on one device (several streams or threads)
+ * race, and must be ordered by the caller.  The first call on a device looks
+ * up the array's device address (not under graph capture).
+ * ------------------------------------------------------------------------ */
+size_t mi_decode_static_capacity(void);
+
+int mi_decode_static(const void* q, int64_t q_stride_batch, int64_t q_stride_head,
+                     const void* paged_kv_cache, int64_t num_pages, const int32_t* kv_indptr,
+                     const int32_t* kv_indices, const int32_t* kv_last_page_len, void* out,
+                     int64_t out_stride_batch, int64_t out_stride_head, int32_t batch_size,
+                     int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                     float sm_scale, mi_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
  * Ragged (varlen) paged prefill attention on bf16 MFMA.
  * Replaces flashinfer.prefill.BatchPrefillWithPagedKVCacheWrapper:
  *   plan  -- scheduler.py:704-716 (qo_indptr, paged_kv_indptr,

@@ -38,6 +38,8 @@
 // launch with no memset.
 #include <math.h>
 
+#include <mutex>
+
 #include "mi_common.h"
 
 namespace {
@@ -1015,4 +1017,70 @@ extern "C" int mi_decode_run(void* workspace, size_t workspace_bytes, const void
   RunKernel k = pick_kernel(head_dim, num_qo_heads / num_kv_heads, waves);
   hipLaunchKernelGGL(k, dim3(run_grid(max_units, waves)), dim3(64 * waves), 0, static_cast<hipStream_t>(stream), rp);
   return mi::check_launch("decode_run_kernel");
+}
+
+// ------------------------------------------------------------------ no caller workspace
+// Decode attention for callers that cannot allocate (code under graph capture
+// that may not call hipMalloc, allocation-free serving loops): plan and run
+// in one call, the work list in a static device array instead of a
+// caller-supplied workspace.  Every call on a device shares that device's
+// array, so calls that overlap on one device (other streams, other threads)
+// race; the plan rewrites everything the run reads, and its per-(request,
+// KV head) counters start at zero on every call.
+namespace {
+
+constexpr size_t kStaticScratchBytes = size_t(16) << 20;
+__device__ __attribute__((aligned(256))) char scratch[kStaticScratchBytes];
+
+// Device address of `scratch`, looked up once per device with that device
+// current (the host-side name is only a stand-in for the symbol).
+void* scratch_address(int device) {
+  static std::mutex mu;
+  static void* addr[64] = {nullptr};
+  if (device < 0 || device >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[device]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    addr[device] = ptr;
+  }
+  return addr[device];
+}
+
+}  // namespace
+
+extern "C" size_t mi_decode_static_capacity(void) { return kStaticScratchBytes; }
+
+extern "C" int mi_decode_static(const void* q, int64_t q_stride_batch, int64_t q_stride_head,
+                                const void* paged_kv_cache, int64_t num_pages, const int32_t* kv_indptr,
+                                const int32_t* kv_indices, const int32_t* kv_last_page_len, void* out,
+                                int64_t out_stride_batch, int64_t out_stride_head, int32_t batch_size,
+                                int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                float sm_scale, mi_stream_t stream) {
+  mi::clear_error();
+  int rc = check_shape("decode static", batch_size, num_qo_heads, num_kv_heads, head_dim, page_size);
+  if (rc) return rc;
+  if (batch_size == 0) return MI_OK;
+  // one resident round of units plus one item per request: the work list
+  // the plan needs for this batch, which must fit the static array
+  const int max_units = mi::num_cus() * kUnitsPerCU + batch_size * num_kv_heads;
+  const size_t need = decode_layout(batch_size, num_qo_heads, num_kv_heads, head_dim, max_units).total;
+  if (need > kStaticScratchBytes)
+    return mi::fail(MI_ERR_WORKSPACE,
+                    "decode static: batch %d x %d KV heads (group %d, head_dim %d) needs a %zu-byte work list, "
+                    "over the %zu-byte static scratch; use mi_decode_plan / mi_decode_run with a workspace",
+                    batch_size, num_kv_heads, num_qo_heads / num_kv_heads, head_dim, need, kStaticScratchBytes);
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return mi::fail(MI_ERR_LAUNCH, "decode static: no current device");
+  void* ws = scratch_address(device);
+  if (!ws) return mi::fail(MI_ERR_LAUNCH, "decode static: hipGetSymbolAddress of the scratch array failed");
+  rc = mi_decode_plan(ws, kStaticScratchBytes, kv_indptr, kv_indices, kv_last_page_len, batch_size, num_qo_heads,
+                      num_kv_heads, head_dim, page_size, max_units, stream);
+  if (rc) return rc;
+  return mi_decode_run(ws, kStaticScratchBytes, q, q_stride_batch, q_stride_head, paged_kv_cache, num_pages,
+                       kv_indices, out, out_stride_batch, out_stride_head, batch_size, num_qo_heads, num_kv_heads,
+                       head_dim, page_size, sm_scale, max_units, stream);
 }
