@@ -14,6 +14,9 @@ Modules:
                 (top-p restricted) sampling distribution.
   rope       -- rotate-half RoPE tables and the bf16 op sequence of the
                 reference, and the unfused RoPE-then-append sequence.
+  model      -- the model forward over the paged pool in fp32 (one decode
+                step, and the dense causal forward that pins it); the CPU
+                baseline of the end-to-end decode.
 
 Pinning status per function is recorded in each module's docstring.
 """
