@@ -15,8 +15,12 @@ end-to-end decode (bench.py) and as a checker:
   (model.py:207-216), gather-based paged attention over the request's pages
   (``oracle.attention.decode``, the math of model.py:254-298), o_proj,
   residual, RMSNorm, SiLU-gated MLP, residual; final RMSNorm and the LM head;
+* ``prefill_step`` -- the batched ragged prefill of whole prompts: every
+  prompt token's K / V written to its slot, paged causal attention
+  (``oracle.attention.prefill``), logits of each prompt's last token;
 * ``dense_forward`` -- the same model over a whole sequence with causal
-  attention on dense K / V (no pages), used to pin ``decode_step``.
+  attention on dense K / V (no pages), used to pin ``decode_step`` and
+  ``prefill_step``.
 
 Weights are plain CPU tensors (any float dtype; the arithmetic is fp32):
 ``embed [V, H]``, ``lm_head [V, H]``, ``norm [H]`` and per layer ``in_norm``,
@@ -26,7 +30,9 @@ Weights are plain CPU tensors (any float dtype; the arithmetic is fp32):
 Pinning (tests/test_oracle_model.py): ``decode_step`` run token by token after
 a prompt equals ``dense_forward`` of the same sequence at every new position
 (two formulations: paged gather vs dense causal SDPA, incremental vs whole
-sequence); ``rms_norm`` against its float64 closed form and a constant-row
+sequence); ``prefill_step`` of a ragged batch equals ``dense_forward`` of each
+prompt at its last position, and decode steps after it continue the dense
+forward; ``rms_norm`` against its float64 closed form and a constant-row
 case; ``rope`` by position 0 being the identity and the plane-rotation closed
 form.
 """
@@ -40,6 +46,7 @@ import torch
 import torch.nn.functional as F
 
 from .attention import decode as paged_decode
+from .attention import prefill as paged_prefill
 
 
 @dataclass
@@ -121,6 +128,35 @@ def decode_step(w: Weights, s: Shape, ids: torch.Tensor, positions: torch.Tensor
         x = x + o.reshape(b, -1) @ L["w_o"].float().T
         x = x + _mlp(rms_norm(x, L["post_norm"], s.eps), L)
     return rms_norm(x, w.norm, s.eps) @ w.lm_head.float().T
+
+
+def prefill_step(w: Weights, s: Shape, ids: torch.Tensor, qo_indptr: list, pools: list, indptr: list,
+                 indices: list, last_page_len: list, page_size: int = 16) -> torch.Tensor:
+    """Ragged causal prefill of whole prompts (the batched form of
+    scheduler.py:684-752): ``ids`` [T] holds the prompts back to back
+    (``qo_indptr``), prompt b at positions 0..L_b-1; the CSR describes each
+    request's pages (kv_len = L_b).  Every prompt token's K / V is written to
+    its slot of ``pools[l]``; attention is the oracle's paged causal prefill.
+    Returns fp32 logits of each prompt's last token [B, V]."""
+    nb = len(qo_indptr) - 1
+    lens = [qo_indptr[b + 1] - qo_indptr[b] for b in range(nb)]
+    pos = torch.cat([torch.arange(n) for n in lens])
+    pg = torch.tensor([indices[indptr[b] + p // page_size] for b in range(nb) for p in range(lens[b])])
+    off = pos % page_size
+    x = w.embed[ids].float()
+    for li, L in enumerate(w.layers):
+        h = rms_norm(x, L["in_norm"], s.eps)
+        q, k, v = _qkv(h, L, s)
+        q = rope(q, pos, s.head_dim, s.theta)
+        k = rope(k, pos, s.head_dim, s.theta)
+        pool = pools[li]
+        pool[pg, 0, off] = k.to(pool.dtype)
+        pool[pg, 1, off] = v.to(pool.dtype)
+        o = paged_prefill(q.to(pool.dtype), pool, qo_indptr, indptr, indices, last_page_len, causal=True)
+        x = x + o.reshape(x.shape[0], -1) @ L["w_o"].float().T
+        x = x + _mlp(rms_norm(x, L["post_norm"], s.eps), L)
+    last = torch.tensor([qo_indptr[b + 1] - 1 for b in range(nb)])
+    return rms_norm(x[last], w.norm, s.eps) @ w.lm_head.float().T
 
 
 def dense_forward(w: Weights, s: Shape, ids: torch.Tensor) -> torch.Tensor:

@@ -71,6 +71,42 @@ def test_paged_decode_catches_a_wrong_head_mapping():
     assert not torch.allclose(paged, dense, atol=1e-3, rtol=1e-3)
 
 
+def test_ragged_prefill_then_decode_equals_the_dense_forward():
+    """Two prompts prefilled in one ragged batch (pages interleaved in the
+    pool), then two decode steps of both: the last-prompt-token logits and each
+    decode step's logits equal the dense causal forward of each sequence."""
+    s = om.Shape(hidden=64, heads=6, kv_heads=2, head_dim=16, intermediate=96, vocab=53, theta=10_000.0)
+    w = om.random_weights(s, layers=2, seed=11)
+    for L in w.layers:
+        L["w_qkv"] *= 20
+    g = torch.Generator().manual_seed(5)
+    seqs = [torch.randint(0, s.vocab, (n,), generator=g) for n in (11, 6)]  # prompt + 2 decoded tokens each
+    prompts = [x[:-2] for x in seqs]
+    ps = 4
+    pages = [[6, 1, 4], [3, 0]]  # request 0: 9 prompt + 2 new tokens in 3 pages; request 1: 4 + 2 in 2
+    pools = [torch.zeros(8, 2, ps, s.kv_heads, s.head_dim) for _ in w.layers]
+    qo = [0, len(prompts[0]), len(prompts[0]) + len(prompts[1])]
+
+    def csr(lens):
+        npg = [math.ceil(n / ps) for n in lens]
+        ip = [0, npg[0], npg[0] + npg[1]]
+        ix = pages[0][: npg[0]] + pages[1][: npg[1]]
+        return ip, ix, [n - (p - 1) * ps for n, p in zip(lens, npg)]
+
+    ip, ix, last = csr([len(p) for p in prompts])
+    got = om.prefill_step(w, s, torch.cat(prompts), qo, pools, ip, ix, last, page_size=ps)
+    dense = [om.dense_forward(w, s, x) for x in seqs]
+    for b in range(2):
+        assert torch.allclose(got[b], dense[b][len(prompts[b]) - 1], atol=1e-4, rtol=1e-4)
+    for j in range(2):
+        pos = [len(p) + j for p in prompts]
+        ip, ix, last = csr([p + 1 for p in pos])
+        ids = torch.stack([seqs[b][pos[b]] for b in range(2)])
+        got = om.decode_step(w, s, ids, torch.tensor(pos), pools, ip, ix, last, page_size=ps)
+        for b in range(2):
+            assert torch.allclose(got[b], dense[b][pos[b]], atol=1e-4, rtol=1e-4), (j, b)
+
+
 def test_rms_norm_closed_form():
     x = torch.randn(5, 32, generator=torch.Generator().manual_seed(0), dtype=torch.float64)
     w = torch.rand(32, dtype=torch.float64) + 0.5
