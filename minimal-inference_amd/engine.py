@@ -99,7 +99,8 @@ class _Pinned:
 class Scheduler:
     def __init__(self, model: Model, max_batch_size: int = 8, max_seq_len: int = 4096, page_size: int = 16,
                  num_pages: int | None = None, eos_token_ids: set[int] | None = None, use_graphs: bool = True,
-                 seed: int = 0, workspace_mb: int = 128, zero_released_pages: bool = True, decode_window: int = 1):
+                 seed: int = 0, workspace_mb: int = 128, zero_released_pages: bool = True, decode_window: int = 1,
+                 keep_logits: bool = False):
         cfg = model.cfg
         self.model = model
         self.device = model.device
@@ -146,6 +147,13 @@ class Scheduler:
         self.d_ring = torch.zeros(decode_window, bmax, dtype=torch.int64, device=dev)
         self.d_eos = torch.tensor(sorted(self.eos) or [-1], dtype=torch.int64, device=dev)
         self._ring_host = torch.zeros(decode_window + 1, bmax, dtype=torch.int64).pin_memory()
+        # keep_logits: the last decode step's logits [rows, V] (rows in the
+        # decoding order of that step; copied inside the captured graphs) and
+        # the last prefill's logits of each prompt's last token (admission order)
+        self.keep_logits = keep_logits
+        self.d_logits = torch.empty(bmax, cfg.vocab_size, dtype=model.dtype, device=dev) if keep_logits else None
+        self.p_logits = torch.empty(max_batch_size, cfg.vocab_size, dtype=model.dtype, device=dev) \
+            if keep_logits else None
         self.waiting: deque[Request] = deque()
         self.active: list[Request] = []
         self.free_slots: deque[int] = deque(range(max_batch_size))
@@ -269,6 +277,8 @@ class Scheduler:
         be = self._backend(self.decode_wrapper, "decode", self.d_indptr[: bs + 1], self.d_indices,
                            self.d_last[:bs], self.d_batch[:bs], self.d_pos[:bs])
         logits = self.model.forward(self.d_ids[:bs], self.d_pos[:bs], be)
+        if self.keep_logits:
+            self.d_logits[:bs].copy_(logits)
         return self.sampler.sample(logits, bs, out=self.sampler.out[:bs])
 
     def _plan_decode(self, bs: int) -> None:
@@ -353,6 +363,8 @@ class Scheduler:
         be = self._backend(self.prefill_wrapper, "prefill", self.p_indptr[: n + 1], self.p_indices,
                            self.p_last[:n], bidx, pos)
         logits = self.model.forward(ids, pos, be, last_rows=last_rows)
+        if self.keep_logits:
+            self.p_logits[:n].copy_(logits)
         self.p_sampler.set_params([r.temperature for r in reqs], [r.top_p for r in reqs])
         toks = self.p_sampler.sample(logits, n)
         host = self._fetch(toks, n)

@@ -7,7 +7,7 @@ budgets drawn so that requests retire mid-run and the waiting ones are
 admitted; 100 engine steps.  Every step's decode page table must equal the
 oracle replay of the reference allocator (bit-exact), and the decode
 attention of the last layer on the engine's own pool and page table must
-match the fp32 oracle (max-abs 2e-2) at two points of the run.
+match the fp32 oracle at two points of the run.
 
 Qwen2.5-72B (64 Q / 8 KV heads): (a) the kernels at that shape on a pool the
 size of one layer's share of the HBM left after 145 GB of weights: 48 decode
@@ -15,10 +15,14 @@ requests with contexts log-uniform in [512, 4096] (seed 4) and a ragged
 causal prefill of 8 prompts with lengths uniform in [256, 2048], pages from a
 seeded permutation of the whole pool, vs the fp32 oracle; (b) the engine with
 random-init 72B weights (145 GB) and the page pool sized to the remaining
-HBM: 8 requests decode, then 8 new prompts are prefilled in the same step as
-the decode of the others (prefill then decode, scheduler.py:596-600); page
+HBM: 48 requests decode, then 8 new prompts are prefilled in the same step as
+the decode of all 56 (prefill then decode, scheduler.py:596-600); page
 tables bit-exact vs the oracle replay every step and the last layer's decode
 attention vs the fp32 oracle after the interleaved step.
+
+Attention outputs are checked against the fp32 oracle by max-abs error; each
+case's measured error is recorded (the session's parity table) against its
+bound.
 """
 
 from __future__ import annotations
@@ -32,7 +36,6 @@ from oracle import attention as oatt
 from oracle import paging as opg
 
 pytestmark = pytest.mark.gpu
-TOL = 2e-2
 
 
 def _loguniform(g, n, lo, hi):
@@ -40,7 +43,7 @@ def _loguniform(g, n, lo, hi):
     return [int(round(math.exp(v))) for v in x.tolist()]
 
 
-def _decode_vs_oracle(dev, pool, indptr_d, indices_d, last_d, n, hq, hkv, d, seed):
+def _decode_vs_oracle(dev, parity, pool, indptr_d, indices_d, last_d, n, hq, hkv, d, seed):
     """Decode attention through the wrapper on (pool, CSR of n rows) vs the
     oracle on the used pages copied to the host."""
     from minimal_inference_amd.decode import BatchDecodeWithPagedKVCacheWrapper
@@ -55,9 +58,7 @@ def _decode_vs_oracle(dev, pool, indptr_d, indices_d, last_d, n, hq, hkv, d, see
     used, local = torch.unique(ix, return_inverse=True)
     pool_cpu = pool.index_select(0, used.to(dev)).cpu()
     ref = oatt.decode(q, pool_cpu, ip, local.tolist(), last_d[:n].cpu().tolist())
-    err = (out - ref).abs().max().item()
-    assert err < TOL, err
-    return err
+    return parity(out, ref, f"decode B={n} seed {seed}")
 
 
 def _check_step(sch, res):
@@ -73,7 +74,7 @@ def _check_step(sch, res):
     return n
 
 
-def test_config4_qwen7b_b48_retire_and_admit(dev):
+def test_config4_qwen7b_b48_retire_and_admit(dev, parity):
     from minimal_inference_amd.engine import Request, Scheduler
     from minimal_inference_amd.model import PRESETS, Model
 
@@ -102,7 +103,7 @@ def test_config4_qwen7b_b48_retire_and_admit(dev):
         retired += len(res["released"])
         n = _check_step(sch, res)
         if step in (30, 80) and n:
-            checks.append(_decode_vs_oracle(dev, sch.kv.kv_data[cfg.num_hidden_layers - 1], sch.d_indptr,
+            checks.append(_decode_vs_oracle(dev, parity, sch.kv.kv_data[cfg.num_hidden_layers - 1], sch.d_indptr,
                                             sch.d_indices, sch.d_last, n, cfg.num_attention_heads,
                                             cfg.num_key_value_heads, cfg.head_dim, seed=step))
     assert sch.pt.error_word() == 0
@@ -113,7 +114,7 @@ def test_config4_qwen7b_b48_retire_and_admit(dev):
             assert len(r.generated_tokens) == b or r.current_position >= 4096
 
 
-def test_config5_qwen72b_shapes_large_pool(dev):
+def test_config5_qwen72b_shapes_large_pool(dev, parity):
     """Kernels at the 72B head shape; pool pages spread over a 1.5 GB layer pool."""
     from minimal_inference_amd.prefill import BatchPrefillWithPagedKVCacheWrapper
 
@@ -137,7 +138,7 @@ def test_config5_qwen72b_shapes_large_pool(dev):
 
     ip, ix, last, used = csr(dec_lens, 0)
     i32 = lambda x: torch.tensor(x, dtype=torch.int32, device=dev)
-    _decode_vs_oracle(dev, pool, i32(ip), ix.to(dev), i32(last), 48, hq, hkv, d, seed=41)
+    _decode_vs_oracle(dev, parity, pool, i32(ip), ix.to(dev), i32(last), 48, hq, hkv, d, seed=41)
 
     pip, pix, plast, _ = csr(pre_lens, used)
     qo = [0]
@@ -150,43 +151,50 @@ def test_config5_qwen72b_shapes_large_pool(dev):
     pused, plocal = torch.unique(pix, return_inverse=True)
     pool_cpu = pool.index_select(0, pused.to(dev)).cpu()
     ref = oatt.prefill(q, pool_cpu, qo, pip, plocal.tolist(), plast, causal=True)
-    err = (out - ref).abs().max().item()
-    assert err < TOL, err
+    parity(out, ref, "prefill 8 prompts")
 
 
-def test_config5_qwen72b_engine_interleaved_prefill(dev):
+def test_config5_qwen72b_engine_48_decoding_8_prefilled(dev, parity):
+    """Config 5 at its size: 48 requests (prompts log-uniform in [512, 4096],
+    admitted 8 per step) decode; then 8 new prompts (U[256, 2048]) are
+    prefilled in the same step as the decode of all 56 (prefill then decode,
+    scheduler.py:596-600).  Page tables bit-exact vs the oracle replay every
+    step; the last layer's decode attention vs the fp32 oracle after the
+    interleaved step; every request finishes with its token budget."""
     from minimal_inference_amd.engine import Request, Scheduler
     from minimal_inference_amd.model import PRESETS, Model, kv_pool_bytes_per_page
 
     cfg = PRESETS["qwen2.5-72b"]
-    model = Model(cfg, dev, seed=4, max_positions=4096 + 16)
+    model = Model(cfg, dev, seed=4, max_positions=4096 + 64 + 16)
     torch.cuda.synchronize()
     assert model.weight_bytes() > 140e9
     free, _ = torch.cuda.mem_get_info(dev)
     num_pages = int((free - 24 * 2**30) // kv_pool_bytes_per_page(cfg, 16))   # the rest of the HBM, 24 GiB spare
-    assert num_pages > 8 * 257
+    assert num_pages > 56 * 260
     g = torch.Generator().manual_seed(4)
-    first = _loguniform(g, 8, 512, 4096)
-    second = torch.randint(256, 2049, (8,), generator=g).tolist()
-    lens = first + second
-    budgets = [12] * 8 + [4] * 8
+    dec_lens = _loguniform(g, 48, 512, 4096)
+    pre_lens = torch.randint(256, 2049, (8,), generator=g).tolist()
+    lens = dec_lens + pre_lens
+    budgets = [14] * 48 + [4] * 8
     prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist() for n in lens]
-    sch = Scheduler(model, max_batch_size=16, max_seq_len=4096, num_pages=num_pages, seed=4)
-    trace = opg.SchedulerTrace(16, 4096, 16, max_num_pages=sch.kv.max_num_pages)
+    sch = Scheduler(model, max_batch_size=56, max_seq_len=4096 + 64, num_pages=num_pages, seed=4)
+    trace = opg.SchedulerTrace(56, 4096 + 64, 16, max_num_pages=sch.kv.max_num_pages)
     reqs = [Request(str(i), p, budgets[i], 0.0) for i, p in enumerate(prompts)]
     step = 0
     checked = False
-    while step < 40 and (step < 4 or sch.has_work()):
-        if step in (0, 3):
-            for i in (range(8) if step == 0 else range(8, 16)):
-                sch.submit(reqs[i])
-                trace.submit(opg.TraceRequest(i, lens[i], budgets[i]))
+    while step < 40 and (step < 8 or sch.has_work()):
+        batch = range(8 * step, 8 * step + 8) if step < 6 else range(48, 56) if step == 7 else ()
+        for i in batch:
+            sch.submit(reqs[i])
+            trace.submit(opg.TraceRequest(i, lens[i], budgets[i]))
         sch.step()
         res = trace.step()
         n = _check_step(sch, res)
-        if step == 3:       # prefill of the 8 new prompts, then decode of all 16, in one step
-            assert len(res["prefill"]) == 8 and n == 16
-            _decode_vs_oracle(dev, sch.kv.kv_data[cfg.num_hidden_layers - 1], sch.d_indptr, sch.d_indices,
+        if step == 6:
+            assert n == 48 and not res["prefill"]
+        if step == 7:   # prefill of the 8 new prompts, then decode of all 56, in one step
+            assert len(res["prefill"]) == 8 and n == 56
+            _decode_vs_oracle(dev, parity, sch.kv.kv_data[cfg.num_hidden_layers - 1], sch.d_indptr, sch.d_indices,
                               sch.d_last, n, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim,
                               seed=72)
             checked = True

@@ -81,6 +81,35 @@ def test_config2_page_tables_match_reference_allocator(dev):
     assert all(len(t) == nt for t in toks)
 
 
+def test_config2_greedy_ids_are_argmax_of_the_engine_logits(dev):
+    """Config 2 (Qwen2.5-0.5B, 8 requests staggered every 5 steps, 50 greedy
+    tokens): every id the engine emits -- each prompt's first token from the
+    prefill and every graph-replayed decode step's -- equals torch.argmax
+    (first index on ties) of the logits the engine computed for that row in
+    that step (kept by ``keep_logits``; the copy is inside the graphs)."""
+    from minimal_inference_amd.engine import Request, Scheduler
+
+    model = _qwen05(dev, layers=24)
+    prompts, nt = _workload()
+    sch = Scheduler(model, max_batch_size=8, max_seq_len=1024, keep_logits=True)
+    reqs = [Request(str(i), p, nt, 0.0) for i, p in enumerate(prompts)]
+    step = checked = 0
+    while step < 5 * len(reqs) or sch.has_work():
+        if step % 5 == 0 and step // 5 < len(reqs):
+            sch.submit(reqs[step // 5])
+        if sch.has_work():
+            n_wait = len(sch.waiting)
+            toks = [t for _, t in sch.step()]
+            n_pre = n_wait - len(sch.waiting)
+            if n_pre:
+                assert toks[:n_pre] == sch.p_logits[:n_pre].argmax(-1).tolist(), step
+            n_dec = len(toks) - n_pre
+            assert toks[n_pre:] == sch.d_logits[:n_dec].argmax(-1).tolist(), step
+            checked += len(toks)
+        step += 1
+    assert checked == len(reqs) * nt
+
+
 def _torch_reference_logits(model, ids):
     """Dense causal forward of one prompt with SDPA in fp32 (no paging)."""
     cfg = model.cfg

@@ -1,6 +1,8 @@
 """GPU parity: ragged paged prefill attention (MFMA) vs the fp32 oracle.
 
-Tolerance: max-abs 2e-2 against the fp32 oracle on bf16 inputs.
+Tolerance (the ``parity`` fixture): max-abs 2e-2 against the fp32 oracle on
+bf16 inputs, and max |out - ref| / max(1, |ref|) <= 1.2e-2; each case's errors
+are printed in the session's parity table.
 """
 
 from __future__ import annotations
@@ -12,7 +14,6 @@ from oracle import attention as oatt
 from tests.helpers import make_paged_batch
 
 pytestmark = pytest.mark.gpu
-TOL = 2e-2
 
 
 def _run(dev, b, qo_lens, hq, hkv, d, causal=True, seed=0):
@@ -41,33 +42,33 @@ def _run(dev, b, qo_lens, hq, hkv, d, causal=True, seed=0):
 @pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (32, 8, 128), (28, 4, 128), (64, 8, 128),
                                       (6, 3, 128), (8, 1, 64), (16, 4, 256)])
 @pytest.mark.parametrize("L", [1, 5, 64, 100, 300])
-def test_single_request_causal(dev, hq, hkv, d, L):
+def test_single_request_causal(dev, parity, hq, hkv, d, L):
     b = make_paged_batch([L], hq, hkv, d, seed=L + d)
     out, ref = _run(dev, b, [L], hq, hkv, d, seed=L)
-    assert (out - ref).abs().max().item() < TOL
+    parity(out, ref)
 
 
-def test_ragged_batch(dev):
+def test_ragged_batch(dev, parity):
     lens = [37, 200, 5, 513, 64, 1]
     b = make_paged_batch(lens, 32, 8, 128, seed=9)
     out, ref = _run(dev, b, lens, 32, 8, 128, seed=9)
-    assert (out - ref).abs().max().item() < TOL
+    parity(out, ref)
 
 
-def test_kv_longer_than_q_bottom_right_causal(dev):
+def test_kv_longer_than_q_bottom_right_causal(dev, parity):
     """Chunked-prefill shape: the last qo_len of kv_len tokens are queries."""
     kv_lens = [100, 260, 33]
     qo_lens = [20, 64, 33]
     b = make_paged_batch(kv_lens, 28, 4, 128, seed=4)
     out, ref = _run(dev, b, qo_lens, 28, 4, 128, seed=4)
-    assert (out - ref).abs().max().item() < TOL
+    parity(out, ref)
 
 
-def test_non_causal(dev):
+def test_non_causal(dev, parity):
     lens = [50, 129]
     b = make_paged_batch(lens, 16, 4, 64, seed=6)
     out, ref = _run(dev, b, lens, 16, 4, 64, causal=False, seed=6)
-    assert (out - ref).abs().max().item() < TOL
+    parity(out, ref)
 
 
 def test_first_row_attends_only_to_token0(dev):
@@ -79,7 +80,7 @@ def test_first_row_attends_only_to_token0(dev):
     assert torch.equal(out[0], v0)
 
 
-def test_prefill_then_decode_consistency(dev):
+def test_prefill_then_decode_consistency(dev, parity):
     """The last prefill row equals a decode query over the same context."""
     from minimal_inference_amd.decode import BatchDecodeWithPagedKVCacheWrapper
 
@@ -94,7 +95,7 @@ def test_prefill_then_decode_consistency(dev):
     w.plan(torch.tensor(b["indptr"], dtype=torch.int32, device=dev), b["indices"].to(dev),
            torch.tensor(b["last"], dtype=torch.int32, device=dev), 32, 8, 128, 16)
     dec = w.run(last_q.to(dev), b["pool"].to(dev)).float().cpu()
-    assert (dec - torch.stack([out[76], out[77 + 129]])).abs().max().item() < TOL
+    parity(dec, torch.stack([out[76], out[77 + 129]]))
 
 
 def _poison_tails(b):
@@ -110,9 +111,9 @@ def _poison_tails(b):
 
 
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64)])
-def test_stale_rows_past_the_end_are_not_read(dev, hq, hkv, d):
+def test_stale_rows_past_the_end_are_not_read(dev, parity, hq, hkv, d):
     lens = [37, 100, 5, 250]
     b = _poison_tails(make_paged_batch(lens, hq, hkv, d, seed=21))
     out, ref = _run(dev, b, lens, hq, hkv, d, seed=21)
     assert torch.isfinite(out).all()
-    assert (out - ref).abs().max().item() < TOL
+    parity(out, ref)
