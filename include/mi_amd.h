@@ -250,6 +250,26 @@ int mi_page_table_step(void* state, int32_t num_pages, int32_t max_slots,
                        int64_t indices_capacity, int32_t* last_page_len, int32_t* batch_indices,
                        int32_t* positions, int32_t* released_pages, mi_stream_t stream);
 
+/* mi_page_table_step followed, in the same single-workgroup launch, by
+ * mi_decode_plan of the batch_size (= padded_batch, <= 1024) rows it laid
+ * out, into decode_workspace for num_qo_heads / num_kv_heads / head_dim: the
+ * per-step metadata build (scheduler.py:862-901) and the decode wrapper's
+ * plan() (scheduler.py:905-916) in one launch, with the plan taking the rows'
+ * page counts from on-chip memory.  The decode workspace afterwards holds
+ * exactly what mi_decode_plan would have written for the same CSR, so
+ * mi_decode_run (with the same indices buffer) follows it as it follows
+ * mi_decode_plan.  If the step's ops are malformed, its CSR overflows
+ * indices_capacity or padded_batch != batch_size, the plan is empty and its
+ * header error word is 2. */
+int mi_page_table_step_decode_plan(void* state, int32_t num_pages, int32_t max_slots,
+                                   int32_t max_pages_per_slot, const int32_t* ops, int32_t ops_len,
+                                   int32_t page_size, int32_t* indptr, int32_t* indices,
+                                   int64_t indices_capacity, int32_t* last_page_len,
+                                   int32_t* batch_indices, int32_t* positions, int32_t* released_pages,
+                                   int32_t batch_size, void* decode_workspace, size_t decode_workspace_bytes,
+                                   int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                                   mi_stream_t stream);
+
 /* Byte offset of the sticky error word inside the state buffer. */
 size_t mi_page_table_error_offset(int32_t num_pages, int32_t max_slots,
                                   int32_t max_pages_per_slot);

@@ -85,6 +85,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _c_i32, _c_i32, _c_i32, _vp, _c_i32, _c_i32, _vp, _vp, _c_i64, _vp, _vp, _vp, _vp,
          _vp],
     ),
+    "mi_page_table_step_decode_plan": (
+        ctypes.c_int,
+        [_vp, _c_i32, _c_i32, _c_i32, _vp, _c_i32, _c_i32, _vp, _vp, _c_i64, _vp, _vp, _vp, _vp,
+         _c_i32, _vp, _c_sz, _c_i32, _c_i32, _c_i32, _vp],
+    ),
     "mi_page_table_error_offset": (_c_sz, [_c_i32, _c_i32, _c_i32]),
     "mi_pages_zero": (ctypes.c_int, [_vp, _c_i64, _c_i32, _c_i64, _c_i64, _vp, _c_i32, _vp]),
 }

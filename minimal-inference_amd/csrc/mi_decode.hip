@@ -5,11 +5,9 @@
 // the request's kv_len tokens with KV head h / group for Q head h
 // (model.py:286-295 restates it with repeat_interleave + SDPA).
 //
-// Work decomposition.  plan() cuts every request's page list into `nsplit`
-// contiguous page ranges ("items") so that items x kv_heads ("units") fill
-// one resident round of kUnitsPerCU waves per CU, and copies the first
-// kInlinePages page ids of each item into the item, so a wave starts its page
-// loads right after reading the item.  One 64-lane wave runs one unit and
+// Work decomposition.  plan() (mi_decode_plan.h) cuts every request's page
+// list into contiguous page ranges ("items"); items x kv_heads are the
+// "units" of the run.  One 64-lane wave runs one unit and
 // serves all `group` Q heads of its KV head, so each KV byte is read from HBM
 // once per step; a workgroup of W waves (two for head_dim <= 128 and even
 // kv_heads) runs W neighbouring KV heads of one item and loads their pages
@@ -41,23 +39,13 @@
 #include <mutex>
 
 #include "mi_common.h"
+#include "mi_decode_plan.h"
 
 namespace {
 
-constexpr int kPageSize = 16;
+using namespace mi::dplan;
+
 constexpr float kLazyRescale = 8.0f;  // log2 units
-// Units (waves) per CU in the plan's resident round: 6 measured faster than 8
-// (fewer splits, so less partial traffic and shorter merges) and than 4, 5, 7.
-#ifndef MI_DECODE_UNITS_PER_CU
-#define MI_DECODE_UNITS_PER_CU 6
-#endif
-constexpr int kUnitsPerCU = MI_DECODE_UNITS_PER_CU;
-#ifndef MI_DECODE_MIN_CHUNK
-#define MI_DECODE_MIN_CHUNK 4  // pages per item at least (2, 4, 8: 4 measured best on short contexts)
-#endif
-#ifndef MI_DECODE_MERGE_BUDGET
-#define MI_DECODE_MERGE_BUDGET 40  // average splits x group per (request, KV head) the plan aims under
-#endif
 // Pages in flight per wave: two for head_dim 128 (one page pair; four
 // measured slower on every decode shape here since the workgroups load
 // together), four for 64.
@@ -73,7 +61,6 @@ constexpr int kUnitsPerCU = MI_DECODE_UNITS_PER_CU;
 #ifndef MI_DECODE_RS_PAD
 #define MI_DECODE_RS_PAD 16
 #endif
-constexpr int kInlinePages = 24;
 // s_waitcnt immediate (gfx9 encoding): vmcnt = 0, expcnt = 7, lgkmcnt = 15.
 constexpr int kWaitVmcnt0 = 0x0F70;
 // Buffer resource word 3 for gfx9 raw buffers (32-bit data format, no swizzle).
@@ -81,223 +68,48 @@ constexpr int kBufferWord3 = 0x00020000;
 // Cache-policy operand of the buffer intrinsics: nt (non-temporal / streaming).
 constexpr int kCacheNT = 2;
 
-// One item = a contiguous page range of one request.  Read by a wave with one
-// 4-byte load per lane (lane l gets word l), so the page ids come first.
-struct alignas(128) DecodeItem {
-  int pages[kInlinePages];  // kv_indices[page_begin ..] copied by plan(), -1 past the end
-  int b;                    // request
-  int page_begin;           // absolute position in kv_indices
-  int page_end;
-  int last_valid;  // valid tokens in the item's final page (0 when empty)
-  int split;
-  int nsplit;
-  int item_base;  // item index of split 0 of this request
-  int pad;
-};
-static_assert(sizeof(DecodeItem) == 128, "item is read as 32 lanes x 4 bytes");
-constexpr int kItemB = kInlinePages, kItemBegin = kInlinePages + 1, kItemEnd = kInlinePages + 2,
-              kItemLast = kInlinePages + 3, kItemNsplit = kInlinePages + 5, kItemBase = kInlinePages + 6;
-
-struct DecodeHeader {
-  int num_units;
-  int num_items;
-  int chunk_pages;
-  int error;
-};
-
-struct DecodeLayout {
-  size_t items, counters, pml, po, total;
-  int max_items;
-};
-
-DecodeLayout decode_layout(int batch, int hq, int hkv, int head_dim, int max_units) {
-  const int group = hq / hkv;
-  DecodeLayout L;
-  L.max_items = max_units / hkv;
-  size_t off = 256;  // header
-  L.items = off;
-  off = mi::align_up(off + size_t(L.max_items) * sizeof(DecodeItem), 256);
-  L.counters = off;
-  off = mi::align_up(off + size_t(batch) * hkv * sizeof(int), 256);
-  L.pml = off;
-  off = mi::align_up(off + size_t(max_units) * group * 2 * sizeof(float), 256);
-  L.po = off;
-  off = mi::align_up(off + size_t(max_units) * group * head_dim * sizeof(uint16_t), 256);
-  L.total = off;
-  return L;
-}
-
-// Units the workspace holds when the caller does not fix max_units: all of
-// it, capped at 65536 (enough for 8-page items over ~32M tokens x heads).
-int units_that_fit(size_t bytes, int batch, int hq, int hkv, int head_dim) {
-  const int group = hq / hkv;
-  const size_t fixed = 256 + 2 * 256 + size_t(batch) * hkv * sizeof(int);
-  if (bytes <= fixed) return 0;
-  const size_t per_unit = sizeof(DecodeItem) / size_t(hkv) + 1 + size_t(group) * (2 * sizeof(float) + head_dim * sizeof(uint16_t));
-  size_t n = (bytes - fixed) / per_unit;
-  n = n > 65536 ? 65536 : n;
-  while (n > 0 && decode_layout(batch, hq, hkv, head_dim, int(n)).total > bytes) n -= hkv;
-  return int(n);
-}
-
-int default_max_units(int batch, int hkv) { return 4 * mi::num_cus() * kUnitsPerCU + batch * hkv; }
-
 // ------------------------------------------------------------------ plan
-struct PlanParams {
-  const int32_t* indptr;
-  const int32_t* indices;
-  const int32_t* last_page_len;
-  int batch, hkv, target_units, max_items;
-  DecodeHeader* header;
-  DecodeItem* items;
-  int* counters;
-};
-
-__device__ int block_sum(int v, int* scratch) {
-  // Wave sums by xor-shuffle, then the per-wave partials through LDS.
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  __syncthreads();
-  if (lane == 0) scratch[w] = v;
-  __syncthreads();
-  int s = 0;
-  for (int i = 0; i < int(blockDim.x >> 6); ++i) s += scratch[i];
-  __syncthreads();
-  return s;
-}
-
-__device__ int block_max(int v, int* scratch) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
-  __syncthreads();
-  if (lane == 0) scratch[w] = v;
-  __syncthreads();
-  int s = scratch[0];
-  for (int i = 1; i < int(blockDim.x >> 6); ++i) s = max(s, scratch[i]);
-  __syncthreads();
-  return s;
-}
-
-// Inclusive scan over the block: shuffles inside each wave, then the wave
-// totals through LDS (two barriers).  *total receives the block-wide sum.
-__device__ int block_scan(int v, int* wsum, int* total) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = int(blockDim.x >> 6);
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(v, o);
-    if (lane >= o) v += y;
-  }
-  __syncthreads();  // the previous call's readers are done with wsum
-  if (lane == 63) wsum[w] = v;
-  __syncthreads();
-  int pre = 0, tot = 0;
-  for (int i = 0; i < nw; ++i) {
-    const int s = wsum[i];
-    pre += (i < w) ? s : 0;
-    tot += s;
-  }
-  *total = tot;
-  return v + pre;
-}
-
-__device__ __forceinline__ int request_pages(const PlanParams& p, int b) {
-  return max(0, p.indptr[b + 1] - p.indptr[b]);
-}
-// Items of a request of np pages at q16 / 16 pages per item (q16 in 1/16
-// pages: a fractional item length lets the item count land close to the
-// limit, and items then hold floor or ceil of np / nsplit pages).
-__device__ __forceinline__ int items_of(int np, int q16) { return max(1, (np * 16 + q16 - 1) / q16); }
-
-__global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
-  __shared__ int red[16];
-  __shared__ int scan[1024];
-  __shared__ int s_np[1024], s_pb0[1024], s_lpl[1024];
+// One workgroup: each request's page count, first page and last-page length
+// are read once (into LDS when the batch fits one block), then the shared
+// search and item writer (mi_decode_plan.h).
+__global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanParams p) {
+  __shared__ int s_np[kPlanThreads], s_pb0[kPlanThreads], s_lpl[kPlanThreads];
+  __shared__ int red[2][kPlanThreads / 64];
   const int t = threadIdx.x;
+  if (p.batch <= int(blockDim.x)) {
+    if (t < p.batch) {
+      const int pb0 = p.indptr[t], pb1 = p.indptr[t + 1], lpl = p.last_page_len[t];  // one round trip
+      s_np[t] = max(0, pb1 - pb0);
+      s_pb0[t] = pb0;
+      s_lpl[t] = min(max(lpl, 1), kPageSize);
+    }
+    plan_from_lds(p, s_np, s_pb0, s_lpl);
+    return;
+  }
+  const int lane = t & 63, w = t >> 6, nw = int(blockDim.x >> 6);
   int mx = 0, tot = 0;
   for (int b = t; b < p.batch; b += blockDim.x) {
     const int np = request_pages(p, b);
     mx = max(mx, np);
     tot += np;
   }
-  const int max_np = block_max(mx, red);
-  const long long total_np = block_sum(tot, red);
-  // Pages per item, in 1/16 pages ("q16"): the smallest value whose items
-  // fit the limit, found by binary search (the item count is non-increasing
-  // in q16).  The limit is one resident round of units (target_units /
-  // kv_heads items), so no wave runs a second unit -- or whole rounds when
-  // the batch alone needs more -- and never more items than the workspace
-  // holds.
-  const int round_items = max(1, p.target_units / p.hkv);
-  int limit = ((p.batch + round_items - 1) / round_items) * round_items;
-  limit = min(max(limit, 1), p.max_items);
-  // every q16 below 16 total / limit has more than `limit` items (each
-  // request has at least np * 16 / q16 of them)
-  int hi = 16 * max(max_np, 1);
-  // Items of fewer than MI_DECODE_MIN_CHUNK pages only add merge work: the
-  // splits of short contexts do not need that much parallelism.
-  int lo = min(hi, max(16 * MI_DECODE_MIN_CHUNK, int((16 * total_np + limit - 1) / limit)));
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    int cnt = 0;
-    for (int b = t; b < p.batch; b += blockDim.x) cnt += items_of(request_pages(p, b), mid);
-    if (block_sum(cnt, red) <= limit) hi = mid; else lo = mid + 1;
+  for (int o = 32; o > 0; o >>= 1) {
+    mx = max(mx, __shfl_xor(mx, o));
+    tot += __shfl_xor(tot, o);
   }
-  const int q16 = lo;
-  // Items, 1024 requests at a time: the scan gives each request's first
-  // item, then every thread writes whole items (one item per thread per
-  // round, its inline page ids loaded together), finding the item's request
-  // by binary search over the scan.
-  int running = 0;
-  for (int base = 0; base < p.batch; base += blockDim.x) {
-    const int b = base + t;
-    int np = 0, ns = 0, pb0 = 0, lpl = 1;
-    if (b < p.batch) {
-      pb0 = p.indptr[b];
-      np = max(0, p.indptr[b + 1] - pb0);
-      ns = items_of(np, q16);
-      lpl = min(max(p.last_page_len[b], 1), kPageSize);
-    }
-    s_np[t] = np;
-    s_pb0[t] = pb0;
-    s_lpl[t] = lpl;
-    int chunk_total = 0;
-    scan[t] = block_scan(ns, red, &chunk_total);
-    __syncthreads();  // publishes scan and s_np / s_pb0 / s_lpl
-    for (int idx = t; idx < chunk_total; idx += blockDim.x) {
-      int lo_r = 0, hi_r = int(blockDim.x) - 1;  // request r: the first with scan[r] > idx
-      while (lo_r < hi_r) {
-        const int mid = (lo_r + hi_r) >> 1;
-        if (scan[mid] > idx) hi_r = mid; else lo_r = mid + 1;
-      }
-      const int r = lo_r;
-      const int nsr = scan[r] - (r > 0 ? scan[r - 1] : 0);
-      const int first = running + scan[r] - nsr;
-      if (first + nsr > p.max_items) continue;  // the request does not fit: none of its items
-      const int sp = idx - (scan[r] - nsr);
-      const int npr = s_np[r];
-      DecodeItem it;
-      it.b = base + r;
-      it.page_begin = s_pb0[r] + int((long long)sp * npr / nsr);
-      it.page_end = s_pb0[r] + int((long long)(sp + 1) * npr / nsr);
-      it.last_valid = (npr == 0) ? 0 : (sp == nsr - 1 ? s_lpl[r] : kPageSize);
-      it.split = sp;
-      it.nsplit = nsr;
-      it.item_base = first;
-      it.pad = 0;
-      for (int j = 0; j < kInlinePages; ++j)
-        it.pages[j] = (it.page_begin + j < it.page_end) ? p.indices[it.page_begin + j] : -1;
-      p.items[first + sp] = it;
-    }
-    running += chunk_total;
-    __syncthreads();  // the next round rewrites scan and s_*
+  if (lane == 0) {
+    red[0][w] = mx;
+    red[1][w] = tot;
   }
-  for (int i = t; i < p.batch * p.hkv; i += blockDim.x) p.counters[i] = 0;
-  if (t == 0) {
-    const int items = min(running, p.max_items);
-    p.header->num_items = items;
-    p.header->num_units = items * p.hkv;
-    p.header->chunk_pages = (q16 + 15) / 16;  // the longest item
-    p.header->error = (running > p.max_items) ? 1 : 0;
+  __syncthreads();
+  int max_np = 0;
+  long long total_np = 0;
+  for (int i = 0; i < nw; ++i) {
+    max_np = max(max_np, red[0][i]);
+    total_np += red[1][i];
   }
+  const int q16 = plan_q16(p, s_np, false, max_np, total_np);
+  plan_items(p, q16, false, s_np, s_pb0, s_lpl);
 }
 
 // ------------------------------------------------------------------ run
@@ -932,43 +744,51 @@ extern "C" size_t mi_decode_workspace_size(int32_t batch_size, int32_t num_qo_he
   return decode_layout(batch_size, num_qo_heads, num_kv_heads, head_dim, max_units).total;
 }
 
+int mi::dplan::plan_setup(const char* who, void* workspace, size_t workspace_bytes, int batch, int hq, int hkv,
+                          int head_dim, int page_size, int max_units, PlanParams* pp) {
+  int rc = check_shape(who, batch, hq, hkv, head_dim, page_size);
+  if (rc) return rc;
+  if (max_units <= 0) max_units = units_that_fit(workspace_bytes, batch, hq, hkv, head_dim);
+  const DecodeLayout L = decode_layout(batch, hq, hkv, head_dim, max_units);
+  if (!workspace || workspace_bytes < L.total)
+    return mi::fail(MI_ERR_WORKSPACE, "%s: workspace %zu bytes, need %zu", who, workspace_bytes, L.total);
+  if (L.max_items < batch)
+    return mi::fail(MI_ERR_WORKSPACE, "%s: room for %d units, need at least batch*kv_heads = %d", who, max_units,
+                    batch * hkv);
+  char* ws = static_cast<char*>(workspace);
+  pp->batch = batch;
+  pp->hkv = hkv;
+  // One resident round of units, but at most ~40 / group splits per
+  // (request, KV head) on average: the merge's cost grows with splits x
+  // group (Qwen2.5-7B, group 7: 4 units per CU instead of 6 took ~1 us off).
+  {
+    const int group = hq / hkv;
+    const long long cap = (long long)(MI_DECODE_MERGE_BUDGET / group) * batch * hkv;
+    const int round = mi::num_cus() * kUnitsPerCU;
+    pp->target_units = int(cap < round ? (cap > mi::num_cus() * 2 ? cap : mi::num_cus() * 2) : round);
+  }
+  pp->max_items = L.max_items;
+  pp->header = reinterpret_cast<DecodeHeader*>(ws);
+  pp->items = reinterpret_cast<DecodeItem*>(ws + L.items);
+  pp->counters = reinterpret_cast<int*>(ws + L.counters);
+  return MI_OK;
+}
+
 extern "C" int mi_decode_plan(void* workspace, size_t workspace_bytes, const int32_t* kv_indptr,
                               const int32_t* kv_indices, const int32_t* kv_last_page_len,
                               int32_t batch_size, int32_t num_qo_heads, int32_t num_kv_heads,
                               int32_t head_dim, int32_t page_size, int32_t max_units, mi_stream_t stream) {
   mi::clear_error();
-  int rc = check_shape("decode plan", batch_size, num_qo_heads, num_kv_heads, head_dim, page_size);
+  PlanParams pp;
+  const int rc = mi::dplan::plan_setup("decode plan", workspace, workspace_bytes, batch_size, num_qo_heads,
+                                       num_kv_heads, head_dim, page_size, max_units, &pp);
   if (rc) return rc;
-  if (max_units <= 0) max_units = units_that_fit(workspace_bytes, batch_size, num_qo_heads, num_kv_heads, head_dim);
-  const DecodeLayout L = decode_layout(batch_size, num_qo_heads, num_kv_heads, head_dim, max_units);
-  if (!workspace || workspace_bytes < L.total)
-    return mi::fail(MI_ERR_WORKSPACE, "decode plan: workspace %zu bytes, need %zu", workspace_bytes, L.total);
-  if (L.max_items < batch_size)
-    return mi::fail(MI_ERR_WORKSPACE, "decode plan: room for %d units, need at least batch*kv_heads = %d",
-                    max_units, batch_size * num_kv_heads);
   if (batch_size > 0 && (!kv_indptr || !kv_indices || !kv_last_page_len))
     return mi::fail(MI_ERR_INVALID, "decode plan: null indptr / indices / last_page_len");
-  char* ws = static_cast<char*>(workspace);
-  PlanParams pp;
   pp.indptr = kv_indptr;
   pp.indices = kv_indices;
   pp.last_page_len = kv_last_page_len;
-  pp.batch = batch_size;
-  pp.hkv = num_kv_heads;
-  // One resident round of units, but at most ~40 / group splits per
-  // (request, KV head) on average: the merge's cost grows with splits x
-  // group (Qwen2.5-7B, group 7: 4 units per CU instead of 6 took ~1 us off).
-  {
-    const int group = num_qo_heads / num_kv_heads;
-    const long long cap = (long long)(MI_DECODE_MERGE_BUDGET / group) * batch_size * num_kv_heads;
-    const int round = mi::num_cus() * kUnitsPerCU;
-    pp.target_units = int(cap < round ? (cap > mi::num_cus() * 2 ? cap : mi::num_cus() * 2) : round);
-  }
-  pp.max_items = L.max_items;
-  pp.header = reinterpret_cast<DecodeHeader*>(ws);
-  pp.items = reinterpret_cast<DecodeItem*>(ws + L.items);
-  pp.counters = reinterpret_cast<int*>(ws + L.counters);
-  hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream), pp);
+  hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, static_cast<hipStream_t>(stream), pp);
   return mi::check_launch("decode_plan_kernel");
 }
 

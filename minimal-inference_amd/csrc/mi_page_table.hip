@@ -15,6 +15,7 @@
 // exclusive-scan offsets so the page order is exactly the sequential deque
 // order.  Released pages are zeroed across all layers by mi_pages_zero.
 #include "mi_common.h"
+#include "mi_decode_plan.h"
 
 namespace {
 
@@ -58,22 +59,58 @@ struct StepParams {
   int64_t capacity;
 };
 
-__device__ int scan_incl(int v, int* buf) {
-  const int t = threadIdx.x;
-  buf[t] = v;
-  __syncthreads();
-  for (int o = 1; o < kThreads; o <<= 1) {
-    const int add = t >= o ? buf[t - o] : 0;
-    __syncthreads();
-    buf[t] += add;
-    __syncthreads();
+// Inclusive scans of two values over the block and the OR of a flag:
+// shuffles inside each wave, then the wave totals through LDS (two
+// barriers).  wsum holds 3 x (kThreads / 64) ints.
+__device__ void scan2_incl(int& a, int& b, int flag, int* wsum, int* tot_a, int* tot_b, int* any_flag) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  constexpr int nw = kThreads / 64;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int ya = __shfl_up(a, o), yb = __shfl_up(b, o);
+    if (lane >= o) {
+      a += ya;
+      b += yb;
+    }
   }
-  return buf[t];
+  const bool wave_flag = __ballot(flag) != 0;
+  __syncthreads();  // the previous scan's readers are done with wsum
+  if (lane == 63) {
+    wsum[w] = a;
+    wsum[nw + w] = b;
+    wsum[2 * nw + w] = wave_flag;
+  }
+  __syncthreads();
+  int pa = 0, pb = 0, ta = 0, tb = 0, f = 0;
+  for (int i = 0; i < nw; ++i) {
+    const int sa = wsum[i], sb = wsum[nw + i];
+    if (i < w) {
+      pa += sa;
+      pb += sb;
+    }
+    ta += sa;
+    tb += sb;
+    f |= wsum[2 * nw + i];
+  }
+  a += pa;
+  b += pb;
+  *tot_a = ta;
+  *tot_b = tb;
+  *any_flag = f;
 }
 
-__global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
-  __shared__ int buf[kThreads];
+// One page-table step (release, admit, decode growth, CSR of the padded
+// decode rows) by one workgroup of kThreads.  When row_np is given, thread t
+// also leaves row t's page count, first page and last-page length there
+// (LDS) for a plan in the same launch, and when row_idx is given and the CSR
+// holds at most row_idx_cap page ids, a copy of them there too.  Returns 0
+// when the CSR is complete,
+// 1 when the ops are malformed (nothing done), 2 when the CSR was cut at the
+// indices capacity; the value is the same in every thread.
+__device__ int step_body(const StepParams& p, int* row_np, int* row_pb0, int* row_lpl, int* row_idx,
+                         int row_idx_cap) {
+  __shared__ int buf[3 * (kThreads / 64)];
   __shared__ int s_indptr[kThreads + 1];
+  __shared__ int s_slot[kThreads];  // decode row -> slot
   __shared__ int head, freec, err, rel_off, total;
   const int t = threadIdx.x;
   int32_t* ring = p.st + p.ring;
@@ -100,7 +137,7 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
   __syncthreads();
   if (!ops_ok) {
     if (t == 0) p.st[2] = err | 16;
-    return;
+    return 1;
   }
 
   // 1. release, in order: pages go to the ring tail
@@ -146,11 +183,17 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
     __syncthreads();
   }
 
-  // 3. decode growth, rows in order: ceil((pos + 1) / page_size) pages
+  // 3 + 4. Decode growth, rows in order, to ceil((pos + 1) / page_size)
+  // pages, and the CSR of the padded rows (rows >= n_dec own only the
+  // scratch page).  One scan carries each row's growth and its page count
+  // after growth; when the growth cannot be served the decode rows get no
+  // pages and the CSR holds the padding rows alone (a closed form).
+  const int h0 = head, f0 = freec;
   int s_row = -1, np_row = 0, need = 0, pos_row = 0;
   if (t < n_dec) {
     s_row = dec_slots[t];
     pos_row = dec_pos[t];
+    s_slot[t] = s_row;
     if (s_row >= 0 && s_row < p.max_slots && pos_row >= 0) {
       np_row = slot_np[s_row];
       need = max(0, (pos_row + 1 + p.page_size - 1) / p.page_size - np_row);
@@ -161,54 +204,48 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
   }
   const int bad = need < 0 ? 1 : 0;
   if (need < 0) need = 0;
-  const int incl = scan_incl(need, buf);
-  if (t == kThreads - 1) total = incl;
-  __syncthreads();
-  const int any_bad = __syncthreads_or(bad);
-  const bool grow_ok = !any_bad && total <= freec;
+  int need_incl = need;
+  int rows_incl = (t < padded) ? ((t < n_dec) ? np_row + need : 1) : 0;
+  int need_total, rows_total, any_bad;
+  scan2_incl(need_incl, rows_incl, bad, buf, &need_total, &rows_total, &any_bad);
+  const bool grow_ok = !any_bad && need_total <= f0;
   if (grow_ok && t < n_dec) {
-    const int first = incl - need;
+    const int first = need_incl - need;
     for (int j = 0; j < need; ++j)
-      slot_pages[size_t(s_row) * p.mpps + np_row + j] = ring[(head + first + j) % p.cap];
+      slot_pages[size_t(s_row) * p.mpps + np_row + j] = ring[(h0 + first + j) % p.cap];
     np_row += need;
     slot_np[s_row] = np_row;
   }
-  __syncthreads();
-  if (t == 0) {
-    if (grow_ok) {
-      head = (head + total) % max(p.cap, 1);
-      freec -= total;
-    } else if (n_dec > 0) {
-      err |= 4;
-    }
-  }
-  __syncthreads();
-
-  // 4. CSR over padded rows (rows >= n_dec own only the scratch page)
-  int rows_np = 0;
-  if (t < padded) rows_np = (t < n_dec) ? (grow_ok ? np_row : 0) : 1;
-  const int ip = scan_incl(rows_np, buf);
+  const int new_head = grow_ok ? (h0 + need_total) % max(p.cap, 1) : h0;
+  const int new_free = grow_ok ? f0 - need_total : f0;
+  const int rows_np = (t < padded) ? ((t < n_dec) ? (grow_ok ? np_row : 0) : 1) : 0;
+  const int ip = grow_ok ? rows_incl : (t < padded ? max(0, t - n_dec + 1) : 0);
+  const int tot_pages = grow_ok ? rows_total : padded - n_dec;
   if (t < padded) s_indptr[t + 1] = ip;
   if (t == 0) s_indptr[0] = 0;
-  __syncthreads();
-  const int tot_pages = s_indptr[padded];
+  __syncthreads();  // s_indptr and the grown page lists are visible to every thread
   // padded + 1 entries: with padded == kThreads the last one has no thread of its own
   for (int i = t; i <= padded; i += kThreads) p.indptr[i] = s_indptr[i];
   if (t < padded) {
+    int last = 1;
     if (t < n_dec) {
       const int seq = pos_row + 1;
-      int last = seq % p.page_size;
+      last = seq % p.page_size;
       if (last == 0 && seq > 0) last = p.page_size;
-      p.last_page_len[t] = last;
       p.positions[t] = pos_row;
     } else {
-      p.last_page_len[t] = 1;
       p.positions[t] = 0;
     }
+    p.last_page_len[t] = last;
     p.batch_indices[t] = t;
+    if (row_np) {
+      row_np[t] = rows_np;
+      row_pb0[t] = ip - rows_np;
+      row_lpl[t] = min(max(last, 1), mi::dplan::kPageSize);
+    }
   }
-  if (tot_pages > p.capacity && t == 0) err |= 8;
   const int lim = int(min<int64_t>(tot_pages, p.capacity));
+  const bool copy_idx = row_idx != nullptr && lim <= row_idx_cap;
   for (int idx = t; idx < lim; idx += kThreads) {
     int lo = 0, hi = padded;  // find row r with s_indptr[r] <= idx < s_indptr[r+1]
     while (hi - lo > 1) {
@@ -218,15 +255,48 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
     const int r = lo;
     const int j = idx - s_indptr[r];
     int pg = p.cap;  // scratch page id == num_pages - 1 == cap
-    if (r < n_dec) pg = slot_pages[size_t(dec_slots[r]) * p.mpps + j];
+    if (r < n_dec) pg = slot_pages[size_t(s_slot[r]) * p.mpps + j];
     p.indices[idx] = pg;
+    if (copy_idx) row_idx[idx] = pg;
   }
   __syncthreads();
   if (t == 0) {
-    p.st[0] = head;
-    p.st[1] = freec;
-    p.st[2] = err;
+    p.st[0] = new_head;
+    p.st[1] = new_free;
+    p.st[2] = err | ((!grow_ok && n_dec > 0) ? 4 : 0) | (tot_pages > p.capacity ? 8 : 0);
   }
+  return tot_pages > p.capacity ? 2 : 0;
+}
+
+__global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
+  step_body(p, nullptr, nullptr, nullptr, nullptr, 0);
+}
+
+// Page ids the fused kernel keeps on chip for the plan's items (32 KB).
+constexpr int kLdsPageIds = 8192;
+
+// The step, then the decode plan of its padded rows in the same workgroup:
+// the plan takes each row's page count, first page and last-page length from
+// LDS and the page ids from the indices the step has just written (visible to
+// the workgroup after the step's barriers).  If the step did not lay out a
+// complete CSR of exactly pp.batch rows, the plan is empty with error 2.
+__global__ __launch_bounds__(kThreads) void step_plan_kernel(StepParams p, mi::dplan::PlanParams pp) {
+  __shared__ int s_np[kThreads], s_pb0[kThreads], s_lpl[kThreads];
+  __shared__ int s_idx[kLdsPageIds];
+  const int status = step_body(p, s_np, s_pb0, s_lpl, s_idx, kLdsPageIds);
+  const int padded = p.ops_len >= 4 ? p.ops[3] : -1;
+  if (status != 0 || padded != pp.batch) {
+    if (threadIdx.x == 0) {
+      pp.header->num_units = 0;
+      pp.header->num_items = 0;
+      pp.header->chunk_pages = 0;
+      pp.header->error = 2;
+    }
+    return;
+  }
+  // the items read their page ids from the on-chip copy when the CSR fit it
+  if (pp.batch > 0 && s_pb0[pp.batch - 1] + s_np[pp.batch - 1] <= kLdsPageIds) pp.indices = s_idx;
+  mi::dplan::plan_from_lds(pp, s_np, s_pb0, s_lpl);
 }
 
 __global__ void zero_kernel(uint4* pools, int64_t layer_stride16, int layers, int64_t page16,
@@ -265,6 +335,40 @@ extern "C" int mi_page_table_init(void* state, int32_t num_pages, int32_t max_sl
   return mi::check_launch("page_table init_kernel");
 }
 
+namespace {
+
+int make_step_params(const char* who, void* state, int32_t num_pages, int32_t max_slots, int32_t max_pages_per_slot,
+                     const int32_t* ops, int32_t ops_len, int32_t page_size, int32_t* indptr, int32_t* indices,
+                     int64_t indices_capacity, int32_t* last_page_len, int32_t* batch_indices, int32_t* positions,
+                     int32_t* released_pages, StepParams* sp) {
+  if (!state || !ops || ops_len < 4 || num_pages < 2 || max_slots <= 0 || max_pages_per_slot <= 0 ||
+      page_size <= 0)
+    return mi::fail(MI_ERR_INVALID, "%s: bad arguments", who);
+  if (!indptr || !indices || !last_page_len || !batch_indices || !positions)
+    return mi::fail(MI_ERR_INVALID, "%s: null output", who);
+  const Layout L = layout(num_pages, max_slots, max_pages_per_slot);
+  sp->st = static_cast<int32_t*>(state);
+  sp->cap = num_pages - 1;
+  sp->max_slots = max_slots;
+  sp->mpps = max_pages_per_slot;
+  sp->page_size = page_size;
+  sp->ring = L.ring;
+  sp->slot_np = L.slot_np;
+  sp->slot_pages = L.slot_pages;
+  sp->ops = ops;
+  sp->ops_len = ops_len;
+  sp->indptr = indptr;
+  sp->indices = indices;
+  sp->last_page_len = last_page_len;
+  sp->batch_indices = batch_indices;
+  sp->positions = positions;
+  sp->released = released_pages;
+  sp->capacity = indices_capacity;
+  return MI_OK;
+}
+
+}  // namespace
+
 extern "C" int mi_page_table_step(void* state, int32_t num_pages, int32_t max_slots,
                                   int32_t max_pages_per_slot, const int32_t* ops, int32_t ops_len,
                                   int32_t page_size, int32_t* indptr, int32_t* indices,
@@ -272,32 +376,41 @@ extern "C" int mi_page_table_step(void* state, int32_t num_pages, int32_t max_sl
                                   int32_t* batch_indices, int32_t* positions, int32_t* released_pages,
                                   mi_stream_t stream) {
   mi::clear_error();
-  if (!state || !ops || ops_len < 4 || num_pages < 2 || max_slots <= 0 || max_pages_per_slot <= 0 ||
-      page_size <= 0)
-    return mi::fail(MI_ERR_INVALID, "page table step: bad arguments");
-  if (!indptr || !indices || !last_page_len || !batch_indices || !positions)
-    return mi::fail(MI_ERR_INVALID, "page table step: null output");
-  const Layout L = layout(num_pages, max_slots, max_pages_per_slot);
   StepParams sp;
-  sp.st = static_cast<int32_t*>(state);
-  sp.cap = num_pages - 1;
-  sp.max_slots = max_slots;
-  sp.mpps = max_pages_per_slot;
-  sp.page_size = page_size;
-  sp.ring = L.ring;
-  sp.slot_np = L.slot_np;
-  sp.slot_pages = L.slot_pages;
-  sp.ops = ops;
-  sp.ops_len = ops_len;
-  sp.indptr = indptr;
-  sp.indices = indices;
-  sp.last_page_len = last_page_len;
-  sp.batch_indices = batch_indices;
-  sp.positions = positions;
-  sp.released = released_pages;
-  sp.capacity = indices_capacity;
+  const int rc = make_step_params("page table step", state, num_pages, max_slots, max_pages_per_slot, ops, ops_len,
+                                  page_size, indptr, indices, indices_capacity, last_page_len, batch_indices,
+                                  positions, released_pages, &sp);
+  if (rc) return rc;
   hipLaunchKernelGGL(step_kernel, dim3(1), dim3(kThreads), 0, static_cast<hipStream_t>(stream), sp);
   return mi::check_launch("page_table step_kernel");
+}
+
+extern "C" int mi_page_table_step_decode_plan(void* state, int32_t num_pages, int32_t max_slots,
+                                              int32_t max_pages_per_slot, const int32_t* ops, int32_t ops_len,
+                                              int32_t page_size, int32_t* indptr, int32_t* indices,
+                                              int64_t indices_capacity, int32_t* last_page_len,
+                                              int32_t* batch_indices, int32_t* positions, int32_t* released_pages,
+                                              int32_t batch_size, void* decode_workspace,
+                                              size_t decode_workspace_bytes, int32_t num_qo_heads,
+                                              int32_t num_kv_heads, int32_t head_dim, mi_stream_t stream) {
+  mi::clear_error();
+  StepParams sp;
+  int rc = make_step_params("page table step + decode plan", state, num_pages, max_slots, max_pages_per_slot, ops,
+                            ops_len, page_size, indptr, indices, indices_capacity, last_page_len, batch_indices,
+                            positions, released_pages, &sp);
+  if (rc) return rc;
+  if (batch_size < 0 || batch_size > kThreads)
+    return mi::fail(MI_ERR_INVALID, "page table step + decode plan: batch %d (1..%d padded rows)", batch_size,
+                    kThreads);
+  mi::dplan::PlanParams pp;
+  rc = mi::dplan::plan_setup("page table step + decode plan", decode_workspace, decode_workspace_bytes, batch_size,
+                             num_qo_heads, num_kv_heads, head_dim, page_size, 0, &pp);
+  if (rc) return rc;
+  pp.indptr = indptr;
+  pp.indices = indices;
+  pp.last_page_len = last_page_len;
+  hipLaunchKernelGGL(step_plan_kernel, dim3(1), dim3(kThreads), 0, static_cast<hipStream_t>(stream), sp, pp);
+  return mi::check_launch("page_table step_plan_kernel");
 }
 
 extern "C" int mi_pages_zero(void* pools, int64_t layer_stride_bytes, int32_t num_layers, int64_t num_pages,

@@ -68,6 +68,17 @@ class BatchDecodeWithPagedKVCacheWrapper:
         kv_dtype = kv_data_type or data_type or q_data_type
         if q_data_type != torch.bfloat16 or kv_dtype != torch.bfloat16:
             raise ValueError("decode attention is built for bf16 q and kv")
+        self._check_plan_args(indptr, indices, last_page_len, num_qo_heads, num_kv_heads)
+        batch = indptr.numel() - 1
+        _lib.call(
+            "mi_decode_plan", self._ws.data_ptr(), self._ws_bytes, indptr.data_ptr(),
+            indices.data_ptr(), last_page_len.data_ptr(), batch, num_qo_heads, num_kv_heads, head_dim, page_size, 0,
+            stream_of(indptr),
+        )
+        self._adopt_plan(indptr, indices, last_page_len, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale)
+
+    @staticmethod
+    def _check_plan_args(indptr, indices, last_page_len, num_qo_heads: int, num_kv_heads: int) -> None:
         for n, t in (("indptr", indptr), ("indices", indices), ("last_page_len", last_page_len)):
             require_i32_vector(n, t)
         batch = indptr.numel() - 1
@@ -75,12 +86,13 @@ class BatchDecodeWithPagedKVCacheWrapper:
             raise ValueError("indptr must have batch+1 entries and last_page_len batch entries")
         if num_qo_heads % num_kv_heads:
             raise ValueError(f"num_qo_heads {num_qo_heads} is not a multiple of num_kv_heads {num_kv_heads}")
-        _lib.call(
-            "mi_decode_plan", self._ws.data_ptr(), self._ws_bytes, indptr.data_ptr(),
-            indices.data_ptr(), last_page_len.data_ptr(), batch, num_qo_heads, num_kv_heads, head_dim, page_size, 0,
-            stream_of(indptr),
-        )
-        self._batch = batch
+
+    def _adopt_plan(self, indptr, indices, last_page_len, num_qo_heads: int, num_kv_heads: int, head_dim: int,
+                    page_size: int, sm_scale: float | None = None) -> None:
+        """Record what run() needs of a plan that has been written into the
+        workspace (by plan(), or by the page-table step that plans the batch
+        it lays out in the same launch)."""
+        self._batch = indptr.numel() - 1
         self._hq, self._hkv, self._d, self._ps = num_qo_heads, num_kv_heads, head_dim, page_size
         self._indices = indices
         self._indptr = indptr

@@ -405,16 +405,18 @@ class Scheduler:
             w -= 1
         self._up_t.upload([r.temperature for r in reqs] + [0.0] * (padded - b), self.sampler.temperature)
         self._up_p.upload([r.top_p for r in reqs] + [1.0] * (padded - b), self.sampler.top_p)
+        cfg = self.model.cfg
+        plan = (self.decode_wrapper, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim)
         for j in range(w):
             rows = [(r.slot, r.current_position + j) for r in reqs]
+            # page-table step and the decode plan of its rows: one launch
             released = self.pt.step([], rows, padded, self.d_indptr, self.d_indices, self.d_last, self.d_batch,
-                                    self.d_pos)
+                                    self.d_pos, decode_plan=plan)
             self._zero_released(released)
             if j == 0:
                 self._up_ids.upload([r.generated_tokens[-1] for r in reqs] + [0] * (padded - b), self.d_ids)
             else:
                 self.d_ids[:padded].copy_(toks[:padded])
-            self._plan_decode(padded)
             if graph is not None:
                 g, out = graph
                 g.replay()

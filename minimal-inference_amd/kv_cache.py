@@ -161,7 +161,7 @@ class DevicePageTable:
     # ---------------------------------------------------------------- device step
     def step(self, admits: list[tuple[int, int]], rows: list[tuple[int, int]], padded: int,
              indptr: torch.Tensor, indices: torch.Tensor, last_page_len: torch.Tensor,
-             batch_indices: torch.Tensor, positions: torch.Tensor) -> int:
+             batch_indices: torch.Tensor, positions: torch.Tensor, decode_plan=None) -> int:
         """One allocator + CSR step; returns the number of pages released.
 
         admits: (slot, npages) popped from the ring in order.
@@ -169,6 +169,12 @@ class DevicePageTable:
                 ceil((position + 1) / page_size) pages and gets
                 seq_len = position + 1.  Rows ``len(rows) .. padded-1`` own the
                 scratch page only.
+        decode_plan: optional (decode wrapper, num_qo_heads, num_kv_heads,
+                head_dim): the wrapper is planned for the ``padded`` rows of
+                this CSR in the same launch as the step (what
+                ``wrapper.plan(indptr[:padded + 1], indices,
+                last_page_len[:padded], ...)`` would do, without a second
+                launch).
         Released pages are zeroed by the caller via ``released`` (the count is
         returned).
         """
@@ -237,12 +243,18 @@ class DevicePageTable:
         evt = torch.cuda.Event()
         evt.record(torch.cuda.current_stream(self.device))
         self._ops_evt[k] = evt
-        _lib.call(
-            "mi_page_table_step", self.state.data_ptr(), self.num_pages, self.max_slots, self.mpps,
-            self._ops_dev.data_ptr(), n, self.page_size, indptr.data_ptr(), indices.data_ptr(),
-            indices.numel(), last_page_len.data_ptr(), batch_indices.data_ptr(), positions.data_ptr(),
-            self.released.data_ptr(), torch.cuda.current_stream(self.device).cuda_stream,
-        )
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        common = (self.state.data_ptr(), self.num_pages, self.max_slots, self.mpps, self._ops_dev.data_ptr(), n,
+                  self.page_size, indptr.data_ptr(), indices.data_ptr(), indices.numel(), last_page_len.data_ptr(),
+                  batch_indices.data_ptr(), positions.data_ptr(), self.released.data_ptr())
+        if decode_plan is None:
+            _lib.call("mi_page_table_step", *common, stream)
+        else:
+            wrapper, hq, hkv, d = decode_plan
+            wrapper._check_plan_args(indptr, indices, last_page_len, hq, hkv)
+            _lib.call("mi_page_table_step_decode_plan", *common, padded, wrapper._ws.data_ptr(), wrapper._ws_bytes,
+                      hq, hkv, d, stream)
+            wrapper._adopt_plan(indptr[: padded + 1], indices, last_page_len[:padded], hq, hkv, d, self.page_size)
         self._pending_release = []
         self.free_count = free
         for s, n in npages.items():

@@ -196,3 +196,54 @@ def test_failed_step_leaves_the_host_mirror_unchanged(dev):
     assert buf[1][:3].cpu().tolist() == [0, 1, 5]
     assert pt.free_count == 39 - 3
     assert pt.error_word() == 0
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64), (28, 4, 128)])
+def test_fused_step_and_plan_equal_step_then_plan(dev, hq, hkv, d):
+    """mi_page_table_step_decode_plan (one launch) writes the CSR that
+    mi_page_table_step writes and the decode workspace that mi_decode_plan
+    then writes, byte for byte, over steps with admissions, growth, releases
+    and graph padding; the decode attention run on either plan is identical."""
+    from minimal_inference_amd.decode import BatchDecodeWithPagedKVCacheWrapper
+    from minimal_inference_amd.kv_cache import DevicePageTable
+
+    ps, max_bs, mpps, num_pages = 16, 40, 80, 3000
+    rng = random.Random(hq * 100 + d)
+    tables, bufs, wrappers = [], [], []
+    for _ in range(2):
+        tables.append(DevicePageTable(num_pages, max_bs, mpps, ps, dev))
+        bufs.append([torch.zeros(n, dtype=torch.int32, device=dev)
+                     for n in (max_bs + 1, max_bs * mpps + 64, max_bs, max_bs, max_bs)])
+        wrappers.append(BatchDecodeWithPagedKVCacheWrapper(torch.zeros(64 << 20, dtype=torch.uint8, device=dev)))
+    pool = torch.randn(num_pages, 2, ps, hkv, d, device=dev).to(torch.bfloat16)
+    pos = {}
+    free_slots = list(range(max_bs))
+    for step in range(12):
+        admits = []
+        for _ in range(rng.randint(0, 6) if step else 24):
+            if not free_slots:
+                break
+            s = free_slots.pop(0)
+            n = rng.randint(1, 500)
+            admits.append((s, math.ceil(n / ps)))
+            pos[s] = n - 1
+        if step % 3 == 2:  # retire a few
+            for s in rng.sample(sorted(pos), k=min(3, len(pos))):
+                for pt in tables:
+                    pt.release(s)
+                del pos[s]
+                free_slots.append(s)
+        for s in pos:
+            pos[s] += rng.randint(0, 20)
+        rows = [(s, p) for s, p in sorted(pos.items())]
+        padded = next(g for g in (1, 2, 4, 8, 16, 32, 40) if g >= len(rows))
+        tables[0].step(admits, rows, padded, *bufs[0])
+        wrappers[0].plan(bufs[0][0][: padded + 1], bufs[0][1], bufs[0][2][:padded], hq, hkv, d, ps)
+        tables[1].step(admits, rows, padded, *bufs[1], decode_plan=(wrappers[1], hq, hkv, d))
+        torch.cuda.synchronize()
+        for a, b in zip(bufs[0], bufs[1]):
+            assert torch.equal(a, b), step
+        assert torch.equal(wrappers[0]._ws, wrappers[1]._ws), step
+        q = torch.randn(padded, hq, d, device=dev).to(torch.bfloat16)
+        assert torch.equal(wrappers[0].run(q, pool), wrappers[1].run(q, pool)), step
+    assert tables[0].error_word() == 0 and tables[1].error_word() == 0
