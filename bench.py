@@ -6,13 +6,16 @@ requests with prompt lengths uniform in [128, 1024] and random token ids
 page_size 16; one hipGraph per decode batch size.  All prompts are admitted
 and prefilled (one ragged batch) before timing.
 
-A "step" is one full decode step of the 32-request batch: device page-table
-step, plan(), graph replay (32 layers: GEMMs, RoPE, KV append, split-K paged
-attention, sampler), the feedback of the sampled ids and, once per window of
-``--decode-window`` steps, end-of-sequence detection on the GPU and the
-read-back of the window's ids.  ``value`` is decoded tokens per second over
-exactly ``--steps`` timed steps; ``decode_tok_s_one_step_per_round_trip`` is
-the same over the next ``--steps`` steps with a read-back after every step.
+A "step" is one full decode step of the 32-request batch: the device
+page-table step with the decode plan (one launch), graph replay (32 layers:
+GEMMs, RoPE, KV append, split-K paged attention, sampler), the feedback of
+the sampled ids and, once per window of ``--decode-window`` steps,
+end-of-sequence detection on the GPU and the read-back of the window's ids.
+The engine is pipelined: the next window is enqueued before the host waits
+for the previous window's ids.  ``value`` is decoded tokens per second over
+exactly ``--steps`` timed steps (the last window read back inside the timed
+region); ``decode_tok_s_one_step_per_round_trip`` is the same over the next
+``--steps`` steps with a read-back after every step.
 
 ``roofline`` is measured on the decode-attention kernel alone: after the
 timed steps, the 32 layers' attention launches (the batch's real page tables
@@ -267,14 +270,15 @@ def served_leg(model: str, concurrency=(2, 20, 32), max_tokens: int = 50, runs: 
     cfg = {"model_preset": model, "device": "cuda", "dtype": "bfloat16", "seed": 0,
            "server": {"host": "127.0.0.1", "port": port},
            "scheduler": {"max_seq_len": 4096, "max_batch_size": 40, "page_size": 16, "decode_window": 1,
-                         "use_graphs": True}}
+                         "pipeline": True, "use_graphs": True}}
     (tmp / "server.yaml").write_text(yaml.safe_dump(cfg))
     logf = open(tmp / "server.log", "w")
     proc = subprocess.Popen([sys.executable, "-u", str(ROOT / "minimal-inference_amd" / "server.py"),
                              "--config", str(tmp / "server.yaml")], stdout=logf, stderr=subprocess.STDOUT)
     url = f"http://127.0.0.1:{port}"
     out = {"server": f"{model} random weights, synthetic byte tokenizer, max_batch_size 40, max_seq_len 4096, "
-                     f"page_size 16, one decode step per host round trip",
+                     f"page_size 16, one decode step per host round trip, pipelined (each step enqueued before the "
+                     f"previous step's ids are read)",
            "prompt": "Write a short poem about the ocean", "max_tokens": max_tokens, "temperature": 0, "runs": runs}
     try:
         t0 = time.time()
@@ -793,7 +797,8 @@ def mistral_leg(args, dev, with_cpu: bool) -> dict:
     model = Model(cfg, dev, seed=args.seed, max_positions=max_seq + 16)
     torch.cuda.synchronize()
     log(f"weights {model.weight_bytes() / 1e9:.2f} GB in {time.time() - t0:.1f}s; capturing graphs")
-    sch = Scheduler(model, max_batch_size=B, max_seq_len=max_seq, seed=args.seed, decode_window=args.decode_window)
+    sch = Scheduler(model, max_batch_size=B, max_seq_len=max_seq, seed=args.seed, decode_window=args.decode_window,
+                    pipeline=True)
     reqs = [Request(str(i), p, new_tokens, 0.0 if i % 2 == 0 else 0.7, 1.0 if i % 2 == 0 else 0.9)
             for i, p in enumerate(prompts)]
     for r in reqs:
@@ -801,21 +806,25 @@ def mistral_leg(args, dev, with_cpu: bool) -> dict:
     t0 = time.time()
     sch.decode_window = 1
     sch.step()  # admit + ragged prefill of all 32 prompts + first decode step
+    sch.flush()
     torch.cuda.synchronize()
 
     def decode_steps(n: int, window: int) -> float:
-        """Exactly ``n`` decode steps in windows of ``window``; wall seconds."""
+        """Exactly ``n`` decode steps in windows of ``window`` (the next window
+        enqueued before the last one's ids are read), then the last window
+        read back; wall seconds."""
         torch.cuda.synchronize()
         t = time.perf_counter()
-        done = 0
-        while done < n:
+        first = len(reqs[0].generated_tokens) + sch.in_flight(reqs[0])
+        while (done := len(reqs[0].generated_tokens) + sch.in_flight(reqs[0]) - first) < n:
             sch.decode_window = min(window, n - done)
-            before = len(reqs[0].generated_tokens)
             sch.step()
-            if len(reqs[0].generated_tokens) == before:
+            if len(reqs[0].generated_tokens) + sch.in_flight(reqs[0]) - first == done:
                 raise RuntimeError("no decode progress (requests finished?)")
-            done += len(reqs[0].generated_tokens) - before
+        sch.flush()
         torch.cuda.synchronize()
+        if len(reqs[0].generated_tokens) - first != n:
+            raise RuntimeError("decode step count mismatch")
         return time.perf_counter() - t
 
     log(f"prefill + first decode step {time.time() - t0:.2f}s; warmup {args.warmup} steps")

@@ -21,9 +21,15 @@ What changes relative to the reference:
   own the scratch page, so their K/V appends land there by construction.
 
 Per decode step the host performs one small host->device copy of op lists and
-input ids, launches the page-table kernel, ``plan()`` and the graph, and
-waits once for the sampled ids (needed to stream tokens and detect EOS) --
-or once per window of ``decode_window`` steps (see ``_decode``).
+input ids, launches the page-table step (which plans the decode in the same
+launch) and the graph, and reads the sampled ids back (needed to stream
+tokens and detect EOS) -- once per window of ``decode_window`` steps (see
+``_decode``).  With ``pipeline=True`` the next window is enqueued before the
+host waits for the previous one's ids whenever the batch is unchanged, so
+the GPU never idles while the host books tokens.  Every read-back also
+carries the device page table's sticky error word and the decode plan's
+error word; a nonzero one (host mirror and device state disagree, a plan
+that did not fit) raises RuntimeError.
 
 Serving: ``start()`` runs the step loop in a daemon thread and
 ``submit_request()`` hands requests to it from any thread
@@ -96,11 +102,24 @@ class _Pinned:
         self.evt.record()
 
 
+@dataclass
+class _Window:
+    """A decode window enqueued on the GPU: its rows, length, pinned read-back
+    slot, the event after its read-back, and its last step's sampled ids
+    (a device tensor, the next window's input when the rows stay)."""
+
+    members: list
+    w: int
+    slot: int
+    evt: "torch.cuda.Event"
+    last: torch.Tensor
+
+
 class Scheduler:
     def __init__(self, model: Model, max_batch_size: int = 8, max_seq_len: int = 4096, page_size: int = 16,
                  num_pages: int | None = None, eos_token_ids: set[int] | None = None, use_graphs: bool = True,
                  seed: int = 0, workspace_mb: int = 128, zero_released_pages: bool = True, decode_window: int = 1,
-                 keep_logits: bool = False):
+                 keep_logits: bool = False, pipeline: bool = False):
         cfg = model.cfg
         self.model = model
         self.device = model.device
@@ -146,7 +165,14 @@ class Scheduler:
         # the first step whose id is an end-of-sequence id (computed on the GPU)
         self.d_ring = torch.zeros(decode_window, bmax, dtype=torch.int64, device=dev)
         self.d_eos = torch.tensor(sorted(self.eos) or [-1], dtype=torch.int64, device=dev)
-        self._ring_host = torch.zeros(decode_window + 1, bmax, dtype=torch.int64).pin_memory()
+        # two pinned read-back slots (a window's ids + first-EOS step per row),
+        # so a window's copy never overwrites the one the host has not read;
+        # per slot also the page table's error word and the plan's
+        self._ring_host = [torch.zeros(decode_window + 1, bmax, dtype=torch.int64).pin_memory() for _ in range(2)]
+        self._err_host = [torch.zeros(3, dtype=torch.int32).pin_memory() for _ in range(2)]
+        self._slot = 0
+        self.pipeline = pipeline
+        self._inflight: _Window | None = None
         # keep_logits: the last decode step's logits [rows, V] (rows in the
         # decoding order of that step; copied inside the captured graphs) and
         # the last prefill's logits of each prompt's last token (admission order)
@@ -182,6 +208,19 @@ class Scheduler:
         while self.has_work() and (max_steps is None or n < max_steps):
             self.step()
             n += 1
+        self.flush()
+
+    def flush(self) -> list[tuple[Request, int]]:
+        """Read the decode window in flight (``pipeline``), book and push its
+        tokens and retire the requests it finished."""
+        if self._inflight is None:
+            return []
+        win, self._inflight = self._inflight, None
+        emitted = self._collect(win)
+        for r, t in emitted:
+            self._push_token(r, t)
+        self._retire()
+        return emitted
 
     # ------------------------------------------------------------------ background loop
     def start(self) -> None:
@@ -367,7 +406,7 @@ class Scheduler:
             self.p_logits[:n].copy_(logits)
         self.p_sampler.set_params([r.temperature for r in reqs], [r.top_p for r in reqs])
         toks = self.p_sampler.sample(logits, n)
-        host = self._fetch(toks, n)
+        host = self._fetch(toks, n, self.prefill_wrapper._ws[4:8].view(torch.int32), "a prefill")
         now = time.perf_counter()
         out = []
         for r, t in zip(reqs, host):
@@ -381,6 +420,19 @@ class Scheduler:
                 r.finish_reason = "stop" if t in self.eos else "length"
         return out
 
+    # ------------------------------------------------------------------ decode
+    def in_flight(self, r: Request) -> int:
+        """Tokens of ``r`` in the decode window in flight (enqueued, not yet
+        read back; ``pipeline`` only)."""
+        w = self._inflight
+        return w.w if w is not None and r in w.members else 0
+
+    def _room(self, r: Request) -> int:
+        """Tokens ``r`` may still be given beyond those already enqueued."""
+        pend = self.in_flight(r)
+        return min(r.max_new_tokens - len(r.generated_tokens) - pend,
+                   self.max_seq_len - (r.current_position + pend))
+
     def _decode(self, reqs: list[Request]) -> list[tuple[Request, int]]:
         """Decode W = min(decode_window, tokens any request may still take)
         steps with one host round trip.  Within the window the sampled ids are
@@ -388,32 +440,62 @@ class Scheduler:
         step), each step's page-table step and plan run ahead without waiting,
         and end-of-sequence detection runs on the GPU over the window's ids.
         A row that samples an end-of-sequence id keeps decoding to the end of
-        the window (its extra tokens are dropped, its pages freed at retire)."""
+        the window (its extra tokens are dropped, its pages freed at retire).
+
+        Without ``pipeline`` the window's ids are read back before returning.
+        With it, a window whose rows are the window in flight's is enqueued
+        first (its input ids are the last sampled ids, still on the GPU), then
+        the window in flight is read: the call returns that window's tokens,
+        one window late.  When the rows differ (an admission, a retirement,
+        a request out of budget) the window in flight is read first."""
+        if not self.pipeline:
+            return self._collect(self._enqueue_window(reqs, None))
+        emitted: list[tuple[Request, int]] = []
+        cand = [r for r in reqs if self._room(r) > 0]
+        prev = self._inflight
+        if prev is not None and cand == prev.members:
+            self._inflight = self._enqueue_window(cand, prev)
+            return self._collect(prev)
+        if prev is not None:
+            self._inflight = None
+            emitted += self._collect(prev)
+            cand = [r for r in self.active if r.status == RequestStatus.DECODING and self._room(r) > 0]
+        if cand:
+            self._inflight = self._enqueue_window(cand, None)
+        return emitted
+
+    def _enqueue_window(self, reqs: list[Request], prev: "_Window | None") -> "_Window":
+        """Enqueue one window of decode steps for ``reqs`` and its read-back
+        into a pinned slot (nothing waits here).  With ``prev`` (the window in
+        flight over the same rows) the first step's input ids are prev's last
+        sampled ids, taken on the GPU."""
         b = len(reqs)
         bs = next((g for g in self.graph_sizes if g >= b), None)
         graph = self.graphs.get(bs) if bs is not None else None
         padded = bs if graph is not None else b
         if padded > self.d_batch.numel():
             raise RuntimeError(f"decode batch {b} exceeds the static buffers ({self.d_batch.numel()})")
-        w = min([self.decode_window] + [r.max_new_tokens - len(r.generated_tokens) for r in reqs]
-                + [self.max_seq_len - r.current_position for r in reqs])
+        start = [r.current_position + self.in_flight(r) for r in reqs]
+        w = min([self.decode_window] + [self._room(r) for r in reqs])
         w = max(1, w)
         # shrink the window until the pool covers every row's growth over it
         # (one step that does not fit raises, as allocate_pages does)
-        while w > 1 and sum(max(0, self.pt.pages_needed(r.current_position + w) - self.pt.slot_npages[r.slot])
-                            for r in reqs) > self.pt.free_count:
+        while w > 1 and sum(max(0, self.pt.pages_needed(p + w) - self.pt.slot_npages[r.slot])
+                            for r, p in zip(reqs, start)) > self.pt.free_count:
             w -= 1
-        self._up_t.upload([r.temperature for r in reqs] + [0.0] * (padded - b), self.sampler.temperature)
-        self._up_p.upload([r.top_p for r in reqs] + [1.0] * (padded - b), self.sampler.top_p)
+        if prev is None:
+            self._up_t.upload([r.temperature for r in reqs] + [0.0] * (padded - b), self.sampler.temperature)
+            self._up_p.upload([r.top_p for r in reqs] + [1.0] * (padded - b), self.sampler.top_p)
         cfg = self.model.cfg
         plan = (self.decode_wrapper, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim)
+        toks = prev.last if prev is not None else None
         for j in range(w):
-            rows = [(r.slot, r.current_position + j) for r in reqs]
+            rows = [(r.slot, p + j) for r, p in zip(reqs, start)]
             # page-table step and the decode plan of its rows: one launch
             released = self.pt.step([], rows, padded, self.d_indptr, self.d_indices, self.d_last, self.d_batch,
                                     self.d_pos, decode_plan=plan)
             self._zero_released(released)
-            if j == 0:
+            if toks is None:
                 self._up_ids.upload([r.generated_tokens[-1] for r in reqs] + [0] * (padded - b), self.d_ids)
             else:
                 self.d_ids[:padded].copy_(toks[:padded])
@@ -425,22 +507,52 @@ class Scheduler:
                 toks = self._decode_forward(padded)
             if w > 1:
                 self.d_ring[j, :padded].copy_(toks[:padded])
+        k = self._slot
+        self._slot ^= 1
+        host = self._ring_host[k]
         if w == 1:
-            host_rows = [[t] for t in self._fetch(toks, b)]
-            stops = [0 if row[0] in self.eos else 1 for row in host_rows]
+            host[0, :b].copy_(toks[:b], non_blocking=True)
         else:
             ring = self.d_ring[:w, :b]
             hit = torch.isin(ring, self.d_eos)
             first = torch.where(hit.any(0), hit.to(torch.int8).argmax(0), torch.full_like(ring[0], w))
-            self._ring_host[:w, :b].copy_(ring, non_blocking=True)
-            self._ring_host[w, :b].copy_(first, non_blocking=True)
-            torch.cuda.current_stream(self.device).synchronize()
-            host = self._ring_host[: w + 1, :b].tolist()
+            host[:w, :b].copy_(ring, non_blocking=True)
+            host[w, :b].copy_(first, non_blocking=True)
+        err = self._err_host[k]
+        err[0:1].copy_(self.pt.state[self.pt._err_word: self.pt._err_word + 1], non_blocking=True)
+        err[1:2].copy_(self.decode_wrapper._ws[12:16].view(torch.int32), non_blocking=True)
+        evt = torch.cuda.Event()
+        evt.record(torch.cuda.current_stream(self.device))
+        return _Window(list(reqs), w, k, evt, toks)
+
+    def _check_errors(self, err: list[int], what: str) -> None:
+        if err[0]:
+            raise RuntimeError(f"device page table error bits {err[0]:#x} after {what}: the host's page counts and "
+                               f"the device state disagree (1 release, 2 admission, 4 growth, 8 indices capacity, "
+                               f"16 malformed ops)")
+        if err[1]:
+            raise RuntimeError(f"{what}: plan error {err[1]} (1: work items did not fit the workspace, 2: the "
+                               f"page-table step before it failed)")
+
+    def _collect(self, win: "_Window") -> list[tuple[Request, int]]:
+        """Wait for a window's read-back, check the device error words, book
+        its tokens (requests finished before it keep none)."""
+        win.evt.synchronize()
+        self._check_errors(self._err_host[win.slot].tolist(), "a decode window")
+        w, reqs = win.w, win.members
+        b = len(reqs)
+        host = self._ring_host[win.slot][: w + 1, :b].tolist()
+        if w == 1:
+            host_rows = [[host[0][i]] for i in range(b)]
+            stops = [0 if row[0] in self.eos else 1 for row in host_rows]
+        else:
             host_rows = [[host[j][i] for j in range(w)] for i in range(b)]
             stops = host[w]
         now = time.perf_counter()
         out_list = []
         for i, r in enumerate(reqs):
+            if r.status != RequestStatus.DECODING:
+                continue  # finished (end of sequence) in an earlier window
             take = min(w, stops[i] + 1) if stops[i] < w else w
             for t in host_rows[i][:take]:
                 r.generated_tokens.append(t)
@@ -456,9 +568,18 @@ class Scheduler:
                 raise AssertionError("decode window stopped early without an end-of-sequence id")
         return out_list
 
-    def _fetch(self, toks: torch.Tensor, n: int) -> list[int]:
+    def _fetch(self, toks: torch.Tensor, n: int, ws_err: torch.Tensor | None = None, what: str = "") -> list[int]:
+        """Read ``n`` sampled ids back (one wait), with the page table's error
+        word and, given ``ws_err`` (a device int32 word), a plan's."""
         self._tok_host[:n].copy_(toks[:n], non_blocking=True)
+        err = self._err_host[self._slot]
+        err[0:1].copy_(self.pt.state[self.pt._err_word: self.pt._err_word + 1], non_blocking=True)
+        if ws_err is not None:
+            err[1:2].copy_(ws_err, non_blocking=True)
+        else:
+            err[1] = 0
         torch.cuda.current_stream(self.device).synchronize()
+        self._check_errors(err.tolist(), what)
         return self._tok_host[:n].tolist()
 
     def _retire(self) -> None:

@@ -21,8 +21,8 @@ checkpoint directory) or ``model_preset`` (random weights of a named
 architecture, with the synthetic tokenizer), ``device``, ``dtype``
 (bfloat16), ``seed``, ``server.host`` / ``server.port``,
 ``scheduler.max_seq_len`` / ``max_batch_size`` / ``page_size`` /
-``decode_window`` / ``use_graphs`` (``use_flashinfer`` is accepted and
-ignored: the HIP path is the only one).
+``decode_window`` / ``pipeline`` / ``use_graphs`` (``use_flashinfer`` is
+accepted and ignored: the HIP path is the only one).
 """
 
 from __future__ import annotations
@@ -267,7 +267,7 @@ def init_engine(config: dict):
     sch = Scheduler(model, max_batch_size=int(sc.get("max_batch_size", 40)), max_seq_len=max_seq,
                     page_size=int(sc.get("page_size", 16)), eos_token_ids=stops or None,
                     use_graphs=bool(sc.get("use_graphs", True)), seed=seed,
-                    decode_window=int(sc.get("decode_window", 1)))
+                    decode_window=int(sc.get("decode_window", 1)), pipeline=bool(sc.get("pipeline", False)))
     sch.start()
     return sch, tok, name, stops
 

@@ -110,6 +110,54 @@ def test_config2_greedy_ids_are_argmax_of_the_engine_logits(dev):
     assert checked == len(reqs) * nt
 
 
+@pytest.mark.parametrize("window,pipeline", [(1, True), (4, True), (4, False)])
+def test_pipelined_and_windowed_decode_give_the_same_tokens(dev, window, pipeline):
+    """All requests admitted together with equal budgets, so every decode
+    step has the same rows whatever the mode: the tokens of a decode window of
+    4 and of the pipelined engine (the next window enqueued before the last
+    one's ids are read) equal one-step-per-round-trip decoding."""
+    from minimal_inference_amd.engine import Request, Scheduler
+
+    model = _qwen05(dev, layers=4)
+    prompts, nt = _workload(n=6, new_tokens=21)
+
+    def drive(**kw):
+        sch = Scheduler(model, max_batch_size=8, max_seq_len=1024, **kw)
+        reqs = [Request(str(i), p, nt, 0.0) for i, p in enumerate(prompts)]
+        for r in reqs:
+            sch.submit(r)
+        sch.run()
+        assert not sch.has_work() and sch._inflight is None
+        return [r.generated_tokens for r in reqs]
+
+    ref = drive()
+    assert all(len(t) == nt for t in ref)
+    assert drive(decode_window=window, pipeline=pipeline) == ref
+
+
+@pytest.mark.parametrize("pipeline", [False, True])
+def test_host_device_desync_raises(dev, pipeline):
+    """The host believes pages are free that the device ring does not have:
+    the device refuses the decode growth (its rows get no pages; appends and
+    attention skip them) and the read-back of that step's ids raises,
+    instead of the engine decoding on silently."""
+    from minimal_inference_amd.engine import Request, Scheduler
+
+    model = _qwen05(dev, layers=2)
+    # 5 usable pages: two 30-token prompts take 2 each, growth at position 32
+    # needs 2 more and only 1 is free
+    sch = Scheduler(model, max_batch_size=2, max_seq_len=256, num_pages=6, pipeline=pipeline)
+    g = torch.Generator().manual_seed(3)
+    for i in range(2):
+        sch.submit(Request(str(i), torch.randint(0, 151936, (30,), generator=g).tolist(), 40, 0.0))
+    sch.step()
+    sch.pt.free_count += 10
+    with pytest.raises(RuntimeError, match="page table error"):
+        for _ in range(10):
+            sch.step()
+        sch.flush()
+
+
 def _torch_reference_logits(model, ids):
     """Dense causal forward of one prompt with SDPA in fp32 (no paging)."""
     cfg = model.cfg
