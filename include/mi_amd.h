@@ -197,10 +197,16 @@ int mi_prefill_run(void* workspace, size_t workspace_bytes, const void* q, int64
  * `seed`, with the 64-bit counter *rng_offset (device) advanced once per call
  * on the stream, so graph replays draw fresh numbers.
  * out_tokens: [batch] int64 device.
+ * workspace: device buffer of at least mi_sample_workspace_size(batch_size,
+ * vocab_size) bytes, zero-filled before its first use (the counters in it
+ * are back at zero after every call); one call at a time per workspace.
+ * Each row is split over ceil(vocab / 4096) workgroups in two launches.
  * ------------------------------------------------------------------------ */
+size_t mi_sample_workspace_size(int32_t batch_size, int32_t vocab_size);
+
 int mi_sample(const void* logits, int64_t logits_row_stride, int32_t batch_size, int32_t vocab_size,
               const float* temperature, const float* top_p, uint64_t seed, uint64_t* rng_offset,
-              int64_t* out_tokens, mi_stream_t stream);
+              int64_t* out_tokens, void* workspace, size_t workspace_bytes, mi_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
  * Device page table: FIFO free-page ring + per-slot page lists, and the CSR

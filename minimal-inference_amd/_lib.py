@@ -69,9 +69,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _c_sz, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i32, _c_i64,
          _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_f32, _vp],
     ),
+    "mi_sample_workspace_size": (_c_sz, [_c_i32, _c_i32]),
     "mi_sample": (
         ctypes.c_int,
-        [_vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _c_u64, _vp, _vp, _vp],
+        [_vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _c_u64, _vp, _vp, _vp, _c_sz, _vp],
     ),
     "mi_add_rms_norm": (
         _c_i32,

@@ -9,8 +9,10 @@ softmax + multinomial + argmax + masked index-put; the only host sync is the
 final ``.tolist()``, as in the reference.
 
 ``Sampler`` is the allocation-free form for graph capture: it owns device
-buffers for per-row temperature / top-p, the output ids and the Philox
-counter, so a captured decode step can include the draw.
+buffers for per-row temperature / top-p, the output ids, the Philox counter
+and the kernels' workspace (sized for the largest vocabulary seen, so a call
+before capture sizes it for the captured ones), so a captured decode step can
+include the draw.
 """
 
 from __future__ import annotations
@@ -34,6 +36,15 @@ class Sampler:
         self.temperature = torch.zeros(max_batch, dtype=torch.float32, device=self.device)
         self.top_p = torch.ones(max_batch, dtype=torch.float32, device=self.device)
         self.out = torch.zeros(max_batch, dtype=torch.int64, device=self.device)
+        self.workspace = torch.zeros(0, dtype=torch.uint8, device=self.device)
+
+    def _workspace_for(self, vocab: int) -> torch.Tensor:
+        need = int(_lib.load().mi_sample_workspace_size(self.max_batch, vocab))
+        if self.workspace.numel() < need:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(f"sampler workspace for vocab {vocab} must be sized before graph capture")
+            self.workspace = torch.zeros(need, dtype=torch.uint8, device=self.device)  # counters start at zero
+        return self.workspace
 
     def set_params(self, temperatures, top_p=None) -> None:
         """Copy per-row parameters in (asynchronous host->device copies)."""
@@ -60,10 +71,11 @@ class Sampler:
         if n > self.max_batch:
             raise ValueError(f"{n} rows exceed the sampler's max_batch {self.max_batch}")
         out = self.out if out is None else out
+        ws = self._workspace_for(logits.shape[1])
         _lib.call(
             "mi_sample", logits.data_ptr(), logits.stride(0), n, logits.shape[1],
             self.temperature.data_ptr(), self.top_p.data_ptr() if use_top_p else None,
-            self.seed, self.rng_offset.data_ptr(), out.data_ptr(), stream_of(logits),
+            self.seed, self.rng_offset.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), stream_of(logits),
         )
         return out[:n]
 
