@@ -63,7 +63,7 @@ def parity(request):
         scaled = float((e / ref.float().abs().clamp(min=1.0)).max()) if e.numel() else 0.0
         _PARITY.append((request.node.nodeid, case, err, scaled))
         assert err <= TOL_ABS, f"{request.node.nodeid} {case}: max-abs {err:.3e} > {TOL_ABS:.0e}"
-        assert scaled <= TOL_SCALED, f"{request.node.nodeid} {case}: scaled error {scaled:.3e} > {TOL_SCALED:.0e}"
+        assert scaled <= TOL_SCALED, f"{request.node.nodeid} {case}: scaled error {scaled:.3e} > {TOL_SCALED:.1e}"
         return err
 
     return check
@@ -73,7 +73,7 @@ def pytest_terminal_summary(terminalreporter):
     if not _PARITY:
         return
     tr = terminalreporter
-    tr.section(f"parity vs the fp32 oracle: max-abs (bound {TOL_ABS:.0e}), scaled (bound {TOL_SCALED:.0e})")
+    tr.section(f"parity vs the fp32 oracle: max-abs (bound {TOL_ABS:.0e}), scaled (bound {TOL_SCALED:.1e})")
     for nodeid, case, err, scaled in _PARITY:
         tr.write_line(f"abs {err:.3e}  scaled {scaled:.3e} ({100 * scaled / TOL_SCALED:3.0f}% of bound)  "
                       f"{nodeid} {case}".rstrip())
