@@ -159,3 +159,28 @@ def test_batch_sizes_alternate_on_one_workspace(dev):
                 assert got[i] == want[i], (n, i)
             else:
                 assert 0 <= got[i] < V
+
+
+def test_unaligned_rows_and_partial_last_chunk(dev):
+    """Rows at an odd element stride (2-byte aligned only: the per-token load
+    path) and a vocabulary that ends inside a 4-token group and inside its
+    last 4,096-token chunk: greedy ids stay bit-exact, draws stay inside the
+    nucleus."""
+    V, rows = 9001, 24
+    g = torch.Generator().manual_seed(33)
+    full = (torch.randn(rows, V + 1, generator=g) * 2).to(torch.bfloat16)
+    logits = full[:, :V].contiguous()
+    temps = [0.0 if i % 3 == 0 else 0.8 for i in range(rows)]
+    s = _sampler(dev, rows, seed=3)
+    s.set_params(temps, [0.9] * rows)
+    view = full.to(dev)[:, :V]
+    assert view.stride(0) == V + 1
+    got = s.sample(view).cpu()
+    want = osmp.greedy(logits)
+    sampled = [i for i in range(rows) if temps[i] > 0]
+    probs = osmp.distribution(logits[sampled], [temps[i] for i in sampled], [0.9] * len(sampled))
+    for i in range(rows):
+        if temps[i] == 0.0:
+            assert got[i] == want[i], i
+    for k, i in enumerate(sampled):
+        assert probs[k, got[i]] > 0, (i, int(got[i]))
