@@ -117,3 +117,11 @@ def test_stale_rows_past_the_end_are_not_read(dev, parity, hq, hkv, d):
     out, ref = _run(dev, b, lens, hq, hkv, d, seed=21)
     assert torch.isfinite(out).all()
     parity(out, ref)
+
+
+def test_long_prompt_4096(dev, parity):
+    """One 4,096-token causal prompt: 64 key tiles for the last query rows,
+    the longest per-workgroup loop the bench batches do not reach."""
+    b = make_paged_batch([4096], 8, 2, 128, seed=41)
+    out, ref = _run(dev, b, [4096], 8, 2, 128, seed=41)
+    parity(out, ref)

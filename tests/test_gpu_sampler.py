@@ -184,3 +184,21 @@ def test_unaligned_rows_and_partial_last_chunk(dev):
             assert got[i] == want[i], i
     for k, i in enumerate(sampled):
         assert probs[k, got[i]] > 0, (i, int(got[i]))
+
+
+def test_largest_vocabulary_and_one_past_it(dev):
+    """1,048,576 tokens (256 chunks of 4,096, the most one row may span):
+    greedy ids bit-exact and draws inside the nucleus; one token more is
+    rejected with ValueError before any launch."""
+    V, rows = 1 << 20, 2
+    g = torch.Generator().manual_seed(34)
+    logits = (torch.randn(rows, V, generator=g) * 2).to(torch.bfloat16)
+    logits[0, V - 1] = 30.0  # the greedy row's max in the last chunk's last slot
+    s = _sampler(dev, rows, seed=4)
+    s.set_params([0.0, 0.8], [1.0, 0.5])
+    got = s.sample(logits.to(dev)).cpu()
+    assert int(got[0]) == V - 1 == int(osmp.greedy(logits)[0])
+    probs = osmp.distribution(logits[1:], [0.8], [0.5])
+    assert probs[0, got[1]] > 0
+    with pytest.raises(ValueError, match="vocab"):
+        s.sample(torch.zeros(rows, V + 1, dtype=torch.bfloat16, device=dev))
