@@ -218,13 +218,13 @@ def test_prefill_logits_match_dense_torch(dev):
     assert got.shape == (3, cfg.vocab_size)
 
 
-def _run_window(model, prompts, max_new, window, eos=(), max_seq_len=1024, use_graphs=True):
+def _run_window(model, prompts, max_new, window, eos=(), max_seq_len=1024, use_graphs=True, pipeline=False):
     """All prompts submitted at once; even requests greedy, odd ones
     T=0.7 / top-p 0.9.  Returns (tokens, finish reasons, scheduler)."""
     from minimal_inference_amd.engine import Request, Scheduler
 
     sch = Scheduler(model, max_batch_size=8, max_seq_len=max_seq_len, use_graphs=use_graphs, seed=5,
-                    eos_token_ids=set(eos), decode_window=window)
+                    eos_token_ids=set(eos), decode_window=window, pipeline=pipeline)
     reqs = [Request(str(i), p, max_new[i], 0.0 if i % 2 == 0 else 0.7, 1.0 if i % 2 == 0 else 0.9)
             for i, p in enumerate(prompts)]
     for r in reqs:
@@ -254,6 +254,33 @@ def test_decode_window_matches_single_steps(dev, window):
     assert got == ref
     assert fin == ref_fin
     assert [len(t) for t in got] == max_new[:5] + [21]
+
+
+@pytest.mark.parametrize("window", [1, 4])
+def test_pipelined_end_of_sequence_and_length_limits(dev, window):
+    """Pipelined decoding (each window enqueued before the previous one's ids
+    are read) with requests that stop at an end-of-sequence id and at their
+    own length limits: a stopped request keeps exactly its tokens up to the
+    stop (the window already in flight for it is dropped), the greedy rows
+    match one-step decoding up to that stop (after it the batch differs), the
+    others end at their limits, and every page returns to the pool with no
+    device error."""
+    model = _qwen05(dev, layers=4)
+    prompts, _ = _workload(seed=6, n=6)
+    max_new = [24, 9, 24, 17, 24, 5]
+    ref, ref_fin, _ = _run_window(model, prompts, max_new, 1)
+    i, k, eos = next((i, k, t) for i, toks in enumerate(ref) if i % 2 == 0 for k, t in enumerate(toks)
+                     if k >= 2 and t not in toks[:k] and not any(t in o for j, o in enumerate(ref) if j != i))
+    got, fin, _ = _run_window(model, prompts, max_new, window, eos=[eos], pipeline=True)
+    assert got[i] == ref[i][: k + 1] and fin[i] == "stop"
+    for j in range(len(ref)):
+        if j == i:
+            continue
+        if j % 2 == 0:
+            assert got[j][: k + 1] == ref[j][: k + 1]
+        stopped = eos in got[j]
+        assert fin[j] == ("stop" if stopped else "length")
+        assert stopped or len(got[j]) == max_new[j]
 
 
 def test_decode_window_end_of_sequence(dev):
