@@ -585,22 +585,31 @@ def c2_leg(dev, with_cpu: bool) -> dict:
     lens = torch.randint(32, 257, (8,), generator=g).tolist()
     prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist() for n in lens]
     nt = 50
-    sch = Scheduler(model, max_batch_size=8, max_seq_len=1024, seed=1)
-    reqs = [Request(str(i), p, nt, 0.0) for i, p in enumerate(prompts)]
-    torch.cuda.synchronize()
-    step = toks = 0
-    t0 = time.perf_counter()
-    while step < 5 * len(reqs) or sch.has_work():
-        if step % 5 == 0 and step // 5 < len(reqs):
-            sch.submit(reqs[step // 5])
-        if sch.has_work():
-            toks += len(sch.step())
-        step += 1
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+
+    def run(pipeline: bool):
+        sch = Scheduler(model, max_batch_size=8, max_seq_len=1024, seed=1, pipeline=pipeline)
+        reqs = [Request(str(i), p, nt, 0.0) for i, p in enumerate(prompts)]
+        torch.cuda.synchronize()
+        step = toks = 0
+        t0 = time.perf_counter()
+        while step < 5 * len(reqs) or sch.has_work():
+            if step % 5 == 0 and step // 5 < len(reqs):
+                sch.submit(reqs[step // 5])
+            if sch.has_work():
+                toks += len(sch.step())
+            step += 1
+        toks += len(sch.flush())
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        return reqs, {"tokens": toks, "steps": step, "wall_s": round(wall, 3), "tok_s": round(toks / wall, 1)}
+
+    reqs, gpu = run(False)
+    piped_reqs, piped = run(True)
+    piped["same_tokens"] = [r.generated_tokens for r in piped_reqs] == [r.generated_tokens for r in reqs]
     res = {"workload": "config 2: qwen2.5-0.5b, 8 prompts U[32,256] seed 1, submitted every 5 steps, 50 greedy "
                        "tokens each, one step per host round trip",
-           "gpu": {"tokens": toks, "steps": step, "wall_s": round(wall, 3), "tok_s": round(toks / wall, 1)}}
+           "gpu": gpu,
+           "gpu_pipelined": piped}
     if with_cpu:
         w, s = oracle_weights(model)
         cpu = cpu_staggered_run(w, s, prompts, nt)
@@ -683,8 +692,9 @@ def c4_leg(dev) -> dict:
     budgets = torch.randint(8, 121, (n_req,), generator=g).tolist()
     prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist() for n in lens]
     sch = Scheduler(model, max_batch_size=48, max_seq_len=4096, seed=3)
-    for i, p in enumerate(prompts):
-        sch.submit(Request(str(i), p, budgets[i], 0.0))
+    reqs = [Request(str(i), p, budgets[i], 0.0) for i, p in enumerate(prompts)]
+    for r in reqs:
+        sch.submit(r)
     torch.cuda.synchronize()
     toks = retired = admitted_late = 0
     dec_steps = []
@@ -707,8 +717,33 @@ def c4_leg(dev) -> dict:
     wall = time.perf_counter() - t0
     med = statistics.median(dt for dt, _ in dec_steps) if dec_steps else None
     rows = statistics.median(n for _, n in dec_steps) if dec_steps else None
+    # the same 100 steps with the pipelined read-back (each step enqueued
+    # before the previous one's ids are read; admissions and retirements
+    # read the step in flight first, so the tokens are the same)
+    del sch
+    _free_gpu()
+    psch = Scheduler(model, max_batch_size=48, max_seq_len=4096, seed=3, pipeline=True)
+    preqs = [Request(str(i), p, budgets[i], 0.0) for i, p in enumerate(prompts)]
+    for r in preqs:
+        psch.submit(r)
+    torch.cuda.synchronize()
+    ptoks = 0
+    t0 = time.perf_counter()
+    for _ in range(step + 1):
+        if not psch.has_work():
+            break
+        ptoks += len(psch.step())
+    ptoks += len(psch.flush())
+    torch.cuda.synchronize()
+    pwall = time.perf_counter() - t0
+    same = [r.generated_tokens[: len(q.generated_tokens)] == q.generated_tokens[: len(r.generated_tokens)]
+            for r, q in zip(preqs, reqs)]
+    pipelined = {"steps": step + 1, "tokens": ptoks, "wall_s": round(pwall, 3), "tok_s": round(ptoks / pwall, 1),
+                 "token_prefixes_agree": all(same)}
+    del psch
     return {"workload": "config 4: qwen2.5-7b, B<=48, 64 prompts log-uniform [256,4096] seed 3, budgets U[8,120], "
                         "100 engine steps, one step per host round trip",
+            "pipelined": pipelined,
             "steps": step + 1, "tokens": toks, "wall_s": round(wall, 3), "tok_s": round(toks / wall, 1),
             "admitted_late": admitted_late, "retired": retired, "decode_only_steps": len(dec_steps),
             "decode_only_median_ms": round(med * 1e3, 3) if med else None, "decode_only_median_rows": rows,

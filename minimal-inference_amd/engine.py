@@ -346,6 +346,13 @@ class Scheduler:
     # ------------------------------------------------------------------ step
     def step(self) -> list[tuple[Request, int]]:
         emitted: list[tuple[Request, int]] = []
+        early: list[tuple[Request, int]] = []
+        if (self.pipeline and self._inflight is not None and self.waiting
+                and any(self._room(r) <= 0 for r in self._inflight.members)):
+            # a request of the window in flight ends with it (its budget is
+            # used up): read the window now, so its slot and pages are free
+            # for this step's admissions, as in the unpipelined loop
+            early = self.flush()
         admitted = self._admit()
         if admitted:
             emitted += self._prefill(admitted)
@@ -356,7 +363,7 @@ class Scheduler:
             self._push_token(r, t)
         self._retire()
         self.steps += 1
-        return emitted
+        return early + emitted
 
     def _admit(self) -> list[Request]:
         out = []

@@ -135,6 +135,43 @@ def test_pipelined_and_windowed_decode_give_the_same_tokens(dev, window, pipelin
     assert drive(decode_window=window, pipeline=pipeline) == ref
 
 
+@pytest.mark.parametrize("window", [1, 3])
+def test_pipelined_admissions_after_retirements(dev, window):
+    """More requests than batch slots, with budgets that retire requests at
+    different steps: the pipelined engine reads the window in flight before
+    admitting when one of its requests has used up its budget, so waiting
+    requests are admitted at the same step as in the unpipelined loop, and
+    every request's tokens are the same."""
+    from minimal_inference_amd.engine import Request, Scheduler
+
+    model = _qwen05(dev, layers=4)
+    prompts, _ = _workload(seed=9, n=10)
+    budgets = [5, 12, 7, 20, 3, 9, 15, 6, 11, 4]
+
+    def drive(pipeline):
+        sch = Scheduler(model, max_batch_size=4, max_seq_len=1024, decode_window=window, pipeline=pipeline)
+        reqs = [Request(str(i), p, budgets[i], 0.0) for i, p in enumerate(prompts)]
+        for r in reqs:
+            sch.submit(r)
+        admitted_at, steps = {}, 0
+        while sch.has_work():
+            sch.step()
+            steps += 1
+            for r in reqs:
+                if r.slot >= 0 and r.request_id not in admitted_at:
+                    admitted_at[r.request_id] = steps
+            assert steps < 500
+        sch.flush()
+        assert sch.pt.error_word() == 0
+        return [r.generated_tokens for r in reqs], admitted_at
+
+    ref, ref_at = drive(False)
+    got, got_at = drive(True)
+    assert [len(t) for t in ref] == budgets
+    assert got_at == ref_at
+    assert got == ref
+
+
 @pytest.mark.parametrize("pipeline", [False, True])
 def test_host_device_desync_raises(dev, pipeline):
     """The host believes pages are free that the device ring does not have:
