@@ -266,7 +266,10 @@ int mi_page_table_step(void* state, int32_t num_pages, int32_t max_slots,
  * mi_decode_run (with the same indices buffer) follows it as it follows
  * mi_decode_plan.  If the step's ops are malformed, its CSR overflows
  * indices_capacity or padded_batch != batch_size, the plan is empty and its
- * header error word is 2. */
+ * header error word is 2.  The plan's header error (1: items did not fit the
+ * workspace, 2: no complete CSR to plan) is also ORed, shifted left by 8,
+ * into the state's sticky error word, so a run of steps is checked with one
+ * read of that word. */
 int mi_page_table_step_decode_plan(void* state, int32_t num_pages, int32_t max_slots,
                                    int32_t max_pages_per_slot, const int32_t* ops, int32_t ops_len,
                                    int32_t page_size, int32_t* indptr, int32_t* indices,
@@ -276,7 +279,10 @@ int mi_page_table_step_decode_plan(void* state, int32_t num_pages, int32_t max_s
                                    int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                                    mi_stream_t stream);
 
-/* Byte offset of the sticky error word inside the state buffer. */
+/* Byte offset of the sticky error word inside the state buffer.  Bits: 1 a
+ * release the slot lists disagree with, 2 an admission from an empty ring,
+ * 4 decode growth from an empty ring, 8 a CSR over indices_capacity, 16
+ * malformed ops; 256 / 512 the fused decode plan's errors 1 / 2. */
 size_t mi_page_table_error_offset(int32_t num_pages, int32_t max_slots,
                                   int32_t max_pages_per_slot);
 

@@ -20,6 +20,10 @@
 namespace {
 
 constexpr int kHeaderWords = 16;  // head, free, error, capacity, ...
+// The error word's bits: 1 release, 2 admission, 4 growth, 8 indices
+// capacity, 16 malformed ops (the step); the fused decode plan's error
+// (1 items did not fit, 2 no complete CSR to plan) shifted by this.
+constexpr int kPlanErrorShift = 8;
 constexpr int kThreads = 1024;
 
 struct Layout {
@@ -291,12 +295,19 @@ __global__ __launch_bounds__(kThreads) void step_plan_kernel(StepParams p, mi::d
       pp.header->num_items = 0;
       pp.header->chunk_pages = 0;
       pp.header->error = 2;
+      p.st[2] |= 2 << kPlanErrorShift;  // sticky, beside the step's own bits
     }
     return;
   }
   // the items read their page ids from the on-chip copy when the CSR fit it
   if (pp.batch > 0 && s_pb0[pp.batch - 1] + s_np[pp.batch - 1] <= kLdsPageIds) pp.indices = s_idx;
   mi::dplan::plan_from_lds(pp, s_np, s_pb0, s_lpl);
+  // thread 0 wrote the plan's header: its error, if any, joins the sticky
+  // word, so every step's plan of a decode window is checked at its read-back
+  if (threadIdx.x == 0) {
+    const int perr = pp.header->error;
+    if (perr) p.st[2] |= perr << kPlanErrorShift;
+  }
 }
 
 __global__ void zero_kernel(uint4* pools, int64_t layer_stride16, int layers, int64_t page16,

@@ -67,7 +67,7 @@ class RequestStatus(enum.Enum):
     FINISHED = "finished"
 
 
-@dataclass
+@dataclass(eq=False)  # requests compare by identity (window membership, pipeline bookkeeping)
 class Request:
     request_id: str
     input_ids: list[int]
@@ -149,14 +149,14 @@ class Scheduler:
         self.d_batch = torch.arange(bmax, dtype=torch.int32, device=dev)
         self.d_pos = torch.zeros(bmax, dtype=torch.int32, device=dev)
         self.d_ids = torch.zeros(bmax, dtype=torch.int64, device=dev)
-        self.sampler = Sampler(dev, bmax, seed=seed)
+        self.sampler = Sampler(dev, bmax, seed=seed, vocab=cfg.vocab_size)
         # prefill buffers
         self.p_indptr = torch.zeros(max_batch_size + 1, dtype=torch.int32, device=dev)
         self.p_indices = torch.zeros(max_batch_size * mpps, dtype=torch.int32, device=dev)
         self.p_last = torch.ones(max_batch_size, dtype=torch.int32, device=dev)
         self.p_batch_dummy = torch.zeros(max_batch_size, dtype=torch.int32, device=dev)
         self.p_pos_dummy = torch.zeros(max_batch_size, dtype=torch.int32, device=dev)
-        self.p_sampler = Sampler(dev, max_batch_size, seed=seed + 1)
+        self.p_sampler = Sampler(dev, max_batch_size, seed=seed + 1, vocab=cfg.vocab_size)
         self._up_ids = _Pinned(bmax, torch.int64)
         self._up_t = _Pinned(bmax, torch.float32)
         self._up_p = _Pinned(bmax, torch.float32)
@@ -348,10 +348,11 @@ class Scheduler:
         emitted: list[tuple[Request, int]] = []
         early: list[tuple[Request, int]] = []
         if (self.pipeline and self._inflight is not None and self.waiting
-                and any(self._room(r) <= 0 for r in self._inflight.members)):
-            # a request of the window in flight ends with it (its budget is
-            # used up): read the window now, so its slot and pages are free
-            # for this step's admissions, as in the unpipelined loop
+                and (self.eos or any(self._room(r) <= 0 for r in self._inflight.members))):
+            # a request of the window in flight may end with it (its budget is
+            # used up, or it may sample an end-of-sequence id): read the window
+            # now, so a slot and pages it frees serve this step's admissions,
+            # as in the unpipelined loop
             early = self.flush()
         admitted = self._admit()
         if admitted:
@@ -525,18 +526,22 @@ class Scheduler:
             first = torch.where(hit.any(0), hit.to(torch.int8).argmax(0), torch.full_like(ring[0], w))
             host[:w, :b].copy_(ring, non_blocking=True)
             host[w, :b].copy_(first, non_blocking=True)
+        # the page table's sticky word also holds every step's plan error
         err = self._err_host[k]
         err[0:1].copy_(self.pt.state[self.pt._err_word: self.pt._err_word + 1], non_blocking=True)
-        err[1:2].copy_(self.decode_wrapper._ws[12:16].view(torch.int32), non_blocking=True)
+        err[1] = 0
         evt = torch.cuda.Event()
         evt.record(torch.cuda.current_stream(self.device))
         return _Window(list(reqs), w, k, evt, toks)
 
     def _check_errors(self, err: list[int], what: str) -> None:
-        if err[0]:
+        if err[0] & 0xFF:
             raise RuntimeError(f"device page table error bits {err[0]:#x} after {what}: the host's page counts and "
                                f"the device state disagree (1 release, 2 admission, 4 growth, 8 indices capacity, "
                                f"16 malformed ops)")
+        if err[0] >> 8:
+            raise RuntimeError(f"{what}: decode plan error bits {err[0] >> 8} in a step's fused plan (1: work items "
+                               f"did not fit the workspace, 2: the page-table step before it failed)")
         if err[1]:
             raise RuntimeError(f"{what}: plan error {err[1]} (1: work items did not fit the workspace, 2: the "
                                f"page-table step before it failed)")

@@ -10,9 +10,10 @@ final ``.tolist()``, as in the reference.
 
 ``Sampler`` is the allocation-free form for graph capture: it owns device
 buffers for per-row temperature / top-p, the output ids, the Philox counter
-and the kernels' workspace (sized for the largest vocabulary seen, so a call
-before capture sizes it for the captured ones), so a captured decode step can
-include the draw.
+and the kernels' workspace (sized at construction for ``vocab`` when given,
+else for the largest vocabulary seen; a workspace that grows is replaced but
+kept alive, so a graph captured with the old one never writes into freed
+memory), so a captured decode step can include the draw.
 """
 
 from __future__ import annotations
@@ -28,7 +29,7 @@ _DEFAULT_SEED = 0x6D69616D64  # "miamd"
 class Sampler:
     """Per-device sampler state: rng counter and reusable row buffers."""
 
-    def __init__(self, device: torch.device, max_batch: int, seed: int = _DEFAULT_SEED):
+    def __init__(self, device: torch.device, max_batch: int, seed: int = _DEFAULT_SEED, vocab: int | None = None):
         self.device = torch.device(device)
         self.max_batch = max_batch
         self.seed = int(seed) & 0xFFFFFFFFFFFFFFFF
@@ -37,12 +38,17 @@ class Sampler:
         self.top_p = torch.ones(max_batch, dtype=torch.float32, device=self.device)
         self.out = torch.zeros(max_batch, dtype=torch.int64, device=self.device)
         self.workspace = torch.zeros(0, dtype=torch.uint8, device=self.device)
+        self._retired: list[torch.Tensor] = []  # replaced workspaces a captured graph may still use
+        if vocab is not None:
+            self._workspace_for(vocab)
 
     def _workspace_for(self, vocab: int) -> torch.Tensor:
         need = int(_lib.load().mi_sample_workspace_size(self.max_batch, vocab))
         if self.workspace.numel() < need:
             if torch.cuda.is_current_stream_capturing():
                 raise RuntimeError(f"sampler workspace for vocab {vocab} must be sized before graph capture")
+            if self.workspace.numel():
+                self._retired.append(self.workspace)
             self.workspace = torch.zeros(need, dtype=torch.uint8, device=self.device)  # counters start at zero
         return self.workspace
 

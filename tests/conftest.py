@@ -69,10 +69,28 @@ def parity(request):
     return check
 
 
+# free-form result lines of tests (error tables and the like), printed at the end
+_REPORT: list[tuple[str, str]] = []
+
+
+@pytest.fixture
+def report(request):
+    """``report(line)``: keep a result line for the end-of-session summary."""
+
+    def add(line: str):
+        _REPORT.append((request.node.nodeid, line))
+
+    return add
+
+
 def pytest_terminal_summary(terminalreporter):
+    tr = terminalreporter
+    if _REPORT:
+        tr.section("test reports")
+        for nodeid, line in _REPORT:
+            tr.write_line(f"{nodeid}: {line}")
     if not _PARITY:
         return
-    tr = terminalreporter
     tr.section(f"parity vs the fp32 oracle: max-abs (bound {TOL_ABS:.0e}), scaled (bound {TOL_SCALED:.1e})")
     for nodeid, case, err, scaled in _PARITY:
         tr.write_line(f"abs {err:.3e}  scaled {scaled:.3e} ({100 * scaled / TOL_SCALED:3.0f}% of bound)  "

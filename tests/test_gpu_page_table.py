@@ -247,3 +247,49 @@ def test_fused_step_and_plan_equal_step_then_plan(dev, hq, hkv, d):
         q = torch.randn(padded, hq, d, device=dev).to(torch.bfloat16)
         assert torch.equal(wrappers[0].run(q, pool), wrappers[1].run(q, pool)), step
     assert tables[0].error_word() == 0 and tables[1].error_word() == 0
+
+
+@pytest.mark.parametrize("n_rows,padded,row_pages,hq,hkv,d", [
+    (100, 128, 3, 32, 8, 128),    # 65..1024 rows: the block-wide search and item writer
+    (1000, 1024, 2, 14, 2, 64),   # the largest padded batch, page ids on chip
+    (1000, 1024, 12, 32, 8, 128),  # a CSR of 12,000+ pages, over the 8,192 kept on chip
+])
+def test_fused_step_and_plan_large_batches(dev, n_rows, padded, row_pages, hq, hkv, d):
+    """The fused step + plan on padded batches above 64 rows (the plan's
+    block-wide search over on-chip row data) and on a CSR too large for the
+    on-chip copy of its page ids (the items then read the indices the same
+    workgroup has just written): CSR buffers, the decode workspace and the
+    attention run equal mi_page_table_step followed by mi_decode_plan."""
+    from minimal_inference_amd.decode import BatchDecodeWithPagedKVCacheWrapper
+    from minimal_inference_amd.kv_cache import DevicePageTable
+
+    ps, mpps = 16, row_pages + 2
+    num_pages = n_rows * (row_pages + 1) + 64
+    rng = random.Random(n_rows + row_pages)
+    lens = [rng.randint((row_pages - 1) * ps + 1, row_pages * ps) for _ in range(n_rows)]
+    tables, bufs, wrappers = [], [], []
+    for _ in range(2):
+        tables.append(DevicePageTable(num_pages, n_rows, mpps, ps, dev))
+        bufs.append([torch.zeros(n, dtype=torch.int32, device=dev)
+                     for n in (padded + 1, padded * mpps + 64, padded, padded, padded)])
+        wrappers.append(BatchDecodeWithPagedKVCacheWrapper(torch.zeros(64 << 20, dtype=torch.uint8, device=dev)))
+    admits = [(i, math.ceil(n / ps)) for i, n in enumerate(lens)]
+    for pt, b in zip(tables, bufs):
+        pt.step(admits, [], 0, *b)
+    # one decode step at position len (growth into a new page for the rows whose prompt filled theirs)
+    rows = [(i, n) for i, n in enumerate(lens)]
+    tables[0].step([], rows, padded, *bufs[0])
+    wrappers[0].plan(bufs[0][0][: padded + 1], bufs[0][1], bufs[0][2][:padded], hq, hkv, d, ps)
+    tables[1].step([], rows, padded, *bufs[1], decode_plan=(wrappers[1], hq, hkv, d))
+    torch.cuda.synchronize()
+    total = int(bufs[0][0][padded])
+    assert total >= n_rows * row_pages
+    if row_pages == 12:
+        assert total > 8192
+    for a, b in zip(bufs[0], bufs[1]):
+        assert torch.equal(a, b)
+    assert torch.equal(wrappers[0]._ws, wrappers[1]._ws)
+    pool = torch.randn(num_pages, 2, ps, hkv, d, device=dev).to(torch.bfloat16)
+    q = torch.randn(padded, hq, d, device=dev).to(torch.bfloat16)
+    assert torch.equal(wrappers[0].run(q, pool), wrappers[1].run(q, pool))
+    assert tables[0].error_word() == 0 and tables[1].error_word() == 0

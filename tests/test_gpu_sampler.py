@@ -142,6 +142,72 @@ def test_top_p_boundary_inside_one_bin(dev):
     assert _chi2_ok(counts, probs, rows * calls)
 
 
+def _order_keys(x: torch.Tensor) -> torch.Tensor:
+    """The 16-bit order keys of bf16 values (larger value, larger key); the
+    sampler's coarse bins are key >> 6."""
+    b = x.contiguous().view(torch.int16).to(torch.int32) & 0xFFFF
+    return torch.where((b & 0x8000) != 0, (~b) & 0xFFFF, b | 0x8000)
+
+
+def _multichunk_logits(V, temp, seed, sigma=0.8, ratio=2.0, top=5 * 4096 + 17):
+    """One token at logit 0 (chunk 5) and V - 1 background logits
+    N(-a, sigma) with ``a`` set so that the background holds ``ratio`` times
+    the top token's mass after scaling by 1 / temp: every 4,096-token chunk
+    carries mass, the top token's chunk max lies more than 2^8 above every
+    other chunk's max (so the per-chunk rescale of the coarse bins matters),
+    and the nucleus boundary falls inside the background, in a bin whose
+    tokens come from every chunk."""
+    g = torch.Generator().manual_seed(seed)
+    a = temp * math.log(V / ratio) + sigma * sigma / (2 * temp)
+    x = -a + sigma * torch.randn(V, generator=g)
+    x[top] = 0.0
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("V", [32768, 152064])
+@pytest.mark.parametrize("temp,top_p", [(0.7, 0.9), (1.3, 0.5)])
+def test_distribution_across_chunks(dev, V, temp, top_p):
+    """Vocabularies of 8 and 38 chunks (the configs' 32,768 and 152,064): the
+    cross-chunk path -- per-chunk bins rescaled by 2^(chunk max - row max),
+    the merged-bin boundary search, the race over every chunk -- gives draws
+    that follow the oracle's nucleus distribution.  Checked by chi-square per
+    chunk (the rescale), per distinct scaled value (the weighting and the
+    boundary key, whose tied tokens sit in every chunk), and by support."""
+    C = 4096
+    base = _multichunk_logits(V, temp, seed=V + int(temp * 10))
+    probs = osmp.distribution(base.unsqueeze(0), [temp], [top_p])[0].double()
+    scaled = osmp.scaled_logits(base.unsqueeze(0), [temp])[0]
+    keys = _order_keys(scaled)
+    nchunks = (V + C - 1) // C
+    # the workload has the properties the test is about
+    cmax = torch.stack([scaled[c * C:(c + 1) * C].float().max() for c in range(nchunks)]) * math.log2(math.e)
+    top2 = cmax.sort(descending=True).values[:2]
+    assert float(top2[0] - top2[1]) > 8.0, "chunk maxima must lie more than 2^8 apart"
+    kept = probs > 0
+    kmin = int(keys[kept].min())
+    in_bin = kept & ((keys >> 6) == (kmin >> 6))
+    assert torch.unique(torch.nonzero(in_bin)[:, 0] // C).numel() == nchunks, "boundary bin spans every chunk"
+    assert int((keys == kmin).sum()) > 100 and 0 < int(kept.sum()) < V
+
+    rows, calls = 4096, 32
+    ld = base.to(dev).unsqueeze(0).expand(rows, V).contiguous()
+    s = _sampler(dev, rows, seed=V + 11)
+    s.set_params([temp] * rows, [top_p] * rows)
+    counts = torch.zeros(V, dtype=torch.int64)
+    for _ in range(calls):
+        counts += torch.bincount(s.sample(ld).cpu(), minlength=V)
+    n = rows * calls
+    assert int(counts[~kept].sum()) == 0, "drew a token outside the nucleus"
+    chunk_of = torch.arange(V) // C
+    by_chunk = torch.zeros(nchunks, dtype=torch.int64).index_add_(0, chunk_of, counts)
+    p_chunk = torch.zeros(nchunks, dtype=torch.float64).index_add_(0, chunk_of, probs)
+    assert _chi2_ok(by_chunk.numpy(), p_chunk.numpy(), n), (by_chunk.tolist(), (p_chunk * n).round().tolist())
+    uniq, inv = torch.unique(keys, return_inverse=True)
+    by_key = torch.zeros(uniq.numel(), dtype=torch.int64).index_add_(0, inv, counts)
+    p_key = torch.zeros(uniq.numel(), dtype=torch.float64).index_add_(0, inv, probs)
+    assert _chi2_ok(by_key.numpy(), p_key.numpy(), n)
+
+
 def test_batch_sizes_alternate_on_one_workspace(dev):
     """Calls with different batch sizes share the sampler's workspace (its
     counters sit at fixed offsets): greedy rows stay bit-exact throughout."""
@@ -202,3 +268,28 @@ def test_largest_vocabulary_and_one_past_it(dev):
     assert probs[0, got[1]] > 0
     with pytest.raises(ValueError, match="vocab"):
         s.sample(torch.zeros(rows, V + 1, dtype=torch.bfloat16, device=dev))
+
+
+def test_reference_sample_semantics_on_the_gpu(dev):
+    """The oracle's restatement of sample() (scheduler.py:310-316) against
+    torch's own GPU kernels: a bf16 tensor divided by a Python float (the
+    case where the reciprocal product and the quotient round apart, and every
+    bf16 value in [1, 8) at 0.7), and F.softmax of bf16 logits without a
+    dtype, whose bf16 probabilities lie within one bf16 step of the
+    restatement's (the exponentials' last fp32 bits may differ)."""
+    import torch.nn.functional as F
+
+    x = torch.tensor([2.1765012589443917e-38]).to(torch.bfloat16)
+    assert torch.equal((x.to(dev) / 0.3).cpu(), osmp.scalar_scaled_logits(x, 0.3))
+    r = torch.arange(0x3F80, 0x4100, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    assert torch.equal((r.to(dev) / 0.7).cpu(), osmp.scalar_scaled_logits(r, 0.7))
+    g = torch.Generator().manual_seed(2)
+    logits = (torch.randn(32768, generator=g) * 3).to(torch.bfloat16)
+    s = osmp.scalar_scaled_logits(logits, 0.7)
+    got = F.softmax(s.to(dev), dim=-1).cpu()
+    assert got.dtype == torch.bfloat16
+    want = torch.softmax(s.float(), dim=-1).to(torch.bfloat16)
+    steps = (got.view(torch.int16).int() - want.view(torch.int16).int()).abs()
+    assert int(steps.max()) <= 1
+    p = osmp.sample_distribution(logits, 0.7)
+    assert abs(float(p.sum()) - 1.0) < 1e-12 and torch.equal(p > 0, want > 0)

@@ -128,3 +128,45 @@ def test_rope_identity_and_rotation():
         a, b = x[..., j], x[..., j + d // 2]
         assert torch.allclose(y[..., j], a * c - b * sn, atol=1e-5)
         assert torch.allclose(y[..., j + d // 2], b * c + a * sn, atol=1e-5)
+
+
+def test_decode_mistakes_move_logits_beyond_the_engine_bound():
+    """The end-to-end logits check of the GPU engine (config 2, bound
+    E2E_LOGIT_REL_BOUND on max |engine - oracle| / max |oracle| per step) can
+    see decode mistakes: planted here in the oracle's paged decode at the
+    Qwen2.5-0.5B shape with its N(0, 0.02) weights, a position off by one
+    (RoPE row and append slot) and a new token left out of its own attention
+    each move the logits by more than the bound on every step after the
+    prompt, while the correct paged decode matches the dense forward."""
+    from tests.helpers import E2E_LOGIT_REL_BOUND
+
+    s = om.Shape(896, 14, 2, 64, 4864, 151936)
+    w = om.random_weights(s, layers=4, seed=1)
+    w.lm_head = w.embed
+    g = torch.Generator().manual_seed(1)
+    prompt = torch.randint(0, s.vocab, (40,), generator=g)
+    gen = torch.randint(0, s.vocab, (6,), generator=g)
+    P, ps = prompt.numel(), 16
+    dense = om.dense_forward(w, s, torch.cat([prompt, gen]))[P:]
+
+    def paged(shift=0, drop_new=False):
+        npg = math.ceil((P + gen.numel() + 2) / ps)
+        pools = [torch.zeros(npg, 2, ps, s.kv_heads, s.head_dim, dtype=torch.bfloat16) for _ in w.layers]
+        idx = list(range(npg))
+        np0 = math.ceil(P / ps)
+        om.prefill_step(w, s, prompt, [0, P], pools, [0, np0], idx, [P - (np0 - 1) * ps])
+        out = []
+        for k in range(gen.numel()):
+            pos = P + k
+            n = pos + 1 - (1 if drop_new else 0)  # tokens the attention sees
+            npages = math.ceil(n / ps)
+            out.append(om.decode_step(w, s, gen[k:k + 1], torch.tensor([pos + shift]), pools, [0, npages], idx,
+                                      [n - (npages - 1) * ps])[0])
+        return torch.stack(out)
+
+    def rel(a):
+        return ((a - dense).abs().amax(1) / dense.abs().amax(1))
+
+    assert float(rel(paged()).max()) < 1e-2   # bf16 pool vs fp32 K / V only
+    assert float(rel(paged(shift=1)).min()) > E2E_LOGIT_REL_BOUND
+    assert float(rel(paged(drop_new=True)).min()) > E2E_LOGIT_REL_BOUND

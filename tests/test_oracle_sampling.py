@@ -74,3 +74,35 @@ def test_top_p_hand_case():
     assert (got > 0).tolist() == [True, True, False, False]
     got = osmp.distribution(logits, [1.0], [0.5])[0]
     assert (got > 0).tolist() == [True, False, False, False]
+
+
+def test_sample_keeps_the_float_temperature():
+    """sample() divides by the Python float (0.7 stays 0.7), sample_batch by
+    its bf16 rounding 0.69921875: the scaled logits differ for some inputs."""
+    x = torch.arange(0x3F80, 0x4100, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)  # [1, 8)
+    a = osmp.scalar_scaled_logits(x, 0.7)
+    b = osmp.scaled_logits(x.unsqueeze(0), [0.7])[0]
+    want = (x.double() / 0.7).float().to(torch.bfloat16)  # float64 quotient: same bf16 rounding here
+    assert torch.equal(a, want)
+    assert int((a != b).sum()) > 0
+
+
+def test_sample_reciprocal_product_rounding():
+    """Near the bottom of the fp32 normal range the product with the fp32
+    reciprocal of 0.3 and the quotient round to different bf16 values; the
+    restatement takes the product."""
+    x = torch.tensor([2.1765012589443917e-38]).to(torch.bfloat16)
+    inv = torch.tensor(1.0) / torch.tensor(0.3)
+    assert float(osmp.scalar_scaled_logits(x, 0.3)[0]) == float((x.float() * inv).to(torch.bfloat16)[0])
+    assert float(osmp.scalar_scaled_logits(x, 0.3)[0]) != float((x.float() / 0.3).to(torch.bfloat16)[0])
+
+
+def test_sample_distribution_bf16_probabilities():
+    """Logits [0, bf16(ln 2)] at temperature 1: fp32 softmax (0.33374,
+    0.66626) rounds to bf16 171 * 2^-9 and 171 * 2^-8, which multinomial
+    normalises to exactly 1/3 and 2/3."""
+    x = torch.tensor([0.0, 0.69140625]).to(torch.bfloat16)
+    p = osmp.sample_distribution(x, 1.0)
+    assert p.tolist() == [1 / 3, 2 / 3]
+    assert osmp.sample_distribution(x, 0.0).tolist() == [0.0, 1.0]
+    assert osmp.sample_distribution(torch.tensor([2.0, 2.0, 1.0]), -1.0).tolist() == [1.0, 0.0, 0.0]
