@@ -17,14 +17,22 @@ exactly ``--steps`` timed steps (the last window read back inside the timed
 region); ``decode_tok_s_one_step_per_round_trip`` is the same over the next
 ``--steps`` steps with a read-back after every step.
 
-``roofline`` is measured on the decode-attention kernel alone: after the
-timed steps, the 32 layers' attention launches (the batch's real page tables
-and pools, one pool per layer so nothing is served from the 256 MB Infinity
-Cache) are captured in a hipGraph, replayed ``--attn-iters`` times on the
-current stream and bracketed with HIP events; achieved = algorithmic bytes
-per launch / average launch time.  Algorithmic bytes per launch:
+``roofline`` is measured on the decode step's attention launch, the kernel
+the decode path runs per layer (mi_decode_rope_append_run: RoPE of q and k,
+the new K/V appended to its slot, split-K paged attention): after the timed
+steps, with the CSR of the next decode step (each request's next position
+counted, so the launch writes the slot that step writes anyway), the 32
+layers' launches (the batch's real page tables and pools, one pool per layer
+so nothing is served from the 256 MB Infinity Cache; random qkv rows) are
+captured in a hipGraph, replayed ``--attn-iters`` times on the current stream
+and bracketed with HIP events; achieved = algorithmic bytes per launch /
+average launch time.  Algorithmic bytes per launch (kv_len counts the new
+token, whose K/V comes from the qkv row instead of the pool):
 sum_b kv_len_b * H_kv * D * 2 (K,V) * 2 B + 2 * B * H_q * D * 2 B (q, out)
-+ 4 B * ((B+1) + sum_b npages_b + B) (indptr, indices, last_page_len).
++ 4 B * ((B+1) + sum_b npages_b + B) (indptr, indices, last_page_len)
++ B * H_kv * D * 2 * 2 B (new K, V written) + B * D * 2 * 2 B (cos, sin rows).
+``decode_attn_alone`` times attention alone (mi_decode_run) on the same CSR
+with the first three terms.
 
 ``roofline.traffic`` is the HBM bytes per launch that rocprofv3 counted for
 this same attention leg (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled
@@ -43,11 +51,11 @@ cgroup quota, OMP_NUM_THREADS), and the counts behind it are reported.
 ``cpu_baseline_legs`` adds the oracle's attention alone on one layer of the
 batch (GB/s).
 
-``decode_attn_other_workloads`` times the same decode-attention kernel, the
-same way, on the Qwen2.5-7B (B=48, 28/4 heads) and Qwen2.5-72B (B=48, 64/8
-heads) decode shapes with their log-uniform contexts, and on the Qwen2.5-0.5B
-head shape (14/2 heads, head_dim 64) at B=32 with contexts uniform in
-[512, 4096] (synthetic pools).
+``decode_attn_other_workloads`` times the same launch (and attention alone
+beside it), the same way, on the Qwen2.5-7B (B=48, 28/4 heads) and
+Qwen2.5-72B (B=48, 64/8 heads) decode shapes with their log-uniform contexts,
+and on the Qwen2.5-0.5B head shape (14/2 heads, head_dim 64) at B=32 with
+contexts uniform in [512, 4096] (synthetic pools).
 
 ``config1_decode_attn``: the committed config-1 fixture timed on the HIP
 kernel and on the CPU oracle, and the kernel's error against the fixture.
@@ -74,8 +82,9 @@ the figures the reference's 1,532 tok/s at 32 concurrent is quoted as.
 as repeated launches captured in one hipGraph and replayed between HIP events: the ragged
 causal prefill attention of the 32 prompts for one layer (MFMA bound:
 flops = sum_b 4 * H_q * D * L_b (L_b + 1) / 2, against 2.5 PFLOP/s bf16) and
-of 8 prompts U[256,2048] at the Qwen2.5-72B head shape, the
-decode-step fused RoPE + KV append (into a copy of layer 0's pool), the
+of 8 prompts U[256,2048] at the Qwen2.5-72B head shape, the separate
+RoPE + KV append of 32 decode rows (into a copy of layer 0's pool; the decode
+step folds it into its attention launch), the
 prefill-sized appends of the prompts' rows into their pages (HBM bound against
 8 TB/s; fused RoPE + append bytes = 2 * T * (H_q + 2 H_kv) * D * 2 B (q, k, v
 read and written) + 2 * T * D * 2 B (cos / sin rows) + index ints; plain
@@ -316,14 +325,35 @@ def served_leg(model: str, concurrency=(2, 20, 32), max_tokens: int = 50, runs: 
     return out
 
 
+def decode_attn_bytes(kv_lens, hq, hkv, d) -> int:
+    """Algorithmic bytes of one decode-attention launch: every token's K and
+    V (bf16), q read and out written, the CSR ints."""
+    npages = sum(math.ceil(n / 16) for n in kv_lens)
+    B = len(kv_lens)
+    return sum(kv_lens) * hkv * d * 2 * 2 + 2 * B * hq * d * 2 + 4 * ((B + 1) + npages + B)
+
+
+def decode_step_attn_bytes(kv_lens, hq, hkv, d) -> int:
+    """Algorithmic bytes of the decode step's attention launch with the RoPE
+    and the K/V append folded in (run_rope_append): the attention's bytes --
+    the new token's K and V come from the qkv row instead of the pool, the
+    same count -- plus the new K and V written to their slots and the cos /
+    sin rows read."""
+    B = len(kv_lens)
+    return decode_attn_bytes(kv_lens, hq, hkv, d) + B * hkv * d * 2 * 2 + B * d * 2 * 2
+
+
 def decode_attn_configs(dev) -> list:
-    """Decode attention alone on the other decode workloads' shapes: 32
+    """The decode step's attention launch (RoPE + append + attention) on the
+    other decode workloads' shapes, and attention alone beside it: 32
     synthetic layer pools (pages from a seeded permutation), one plan, the 32
     launches captured in a graph and replayed between HIP events, as in the
-    roofline leg.  Contexts log-uniform as the workloads draw them."""
+    roofline leg.  Contexts (the new token included) log-uniform as the
+    workloads draw them."""
     import torch
 
     from minimal_inference_amd.decode import BatchDecodeWithPagedKVCacheWrapper
+    from minimal_inference_amd.model import precompute_rope
 
     def loguniform(n, lo, hi, seed):
         g = torch.Generator().manual_seed(seed)
@@ -349,22 +379,28 @@ def decode_attn_configs(dev) -> list:
         ip = torch.tensor([0] + torch.tensor(npg).cumsum(0).tolist(), dtype=torch.int32, device=dev)
         lp = torch.tensor([n - (p - 1) * 16 for n, p in zip(lens, npg)], dtype=torch.int32, device=dev)
         qs = [torch.randn(B, hq, d, device=dev, dtype=torch.bfloat16) for _ in range(L)]
+        qkvs = [torch.randn(B, (hq + 2 * hkv) * d, device=dev, dtype=torch.bfloat16) for _ in range(L)]
+        cos, sin = precompute_rope(d, max(lens) + 1, 1e6, dev, torch.bfloat16)
         outs = [torch.empty_like(q) for q in qs]
         w = BatchDecodeWithPagedKVCacheWrapper(torch.empty(128 << 20, dtype=torch.uint8, device=dev))
         w.plan(ip, perm, lp, hq, hkv, d, 16)
-        us = time_us(lambda: [w.run(qs[l], pools[l], out=outs[l]) for l in range(L)], 1) / L
-        nbytes = sum(lens) * hkv * d * 4 + 2 * B * hq * d * 2 + 4 * ((B + 1) + tot + B)
+        # the decode step's launch (RoPE + append + attention), then attention alone
+        us = time_us(lambda: [w.run_rope_append(qkvs[l], cos, sin, pools[l], out=outs[l]) for l in range(L)], 1) / L
+        us_plain = time_us(lambda: [w.run(qs[l], pools[l], out=outs[l]) for l in range(L)], 1) / L
+        nbytes = decode_step_attn_bytes(lens, hq, hkv, d)
+        pbytes = decode_attn_bytes(lens, hq, hkv, d)
         gbps = nbytes / us / 1e3
         out.append({"workload": name, "us": round(us, 2), "mb": round(nbytes / 1e6, 1), "gbps": round(gbps, 1),
-                    "frac": round(gbps / PEAK_HBM_GBPS, 4)})
-        del pools, qs, outs
+                    "frac": round(gbps / PEAK_HBM_GBPS, 4), "attention_alone_us": round(us_plain, 2),
+                    "attention_alone_frac": round(pbytes / us_plain / 1e3 / PEAK_HBM_GBPS, 4)})
+        del pools, qs, qkvs, outs
     return out
 
 
-def measured_traffic(model: str, batch: int, mean_context: float, alg_bytes: float):
+def measured_traffic(kernel: str, model: str, batch: int, mean_context: float, alg_bytes: float):
     """HBM bytes per attention launch from the committed counter record:
-    (bytes, basis), or (None, reason) when the record is for another model or
-    batch.  At the recorded mean context the counted bytes are used as they
+    (bytes, basis), or (None, reason) when the record is for another kernel,
+    model or batch.  At the recorded mean context the counted bytes are used as they
     are; at another context (the steps and warm-up counts move it) the counted
     ratio of HBM bytes to algorithmic bytes is applied to this launch's
     algorithmic bytes -- the extra over the algorithmic bytes is the split
@@ -373,6 +409,8 @@ def measured_traffic(model: str, batch: int, mean_context: float, alg_bytes: flo
         rec = json.loads(TRAFFIC_FILE.read_text())
     except (OSError, ValueError):
         return None, "no counter record"
+    if rec.get("kernel_key") != kernel:
+        return None, f"counter record is for another kernel ({rec.get('kernel')})"
     if rec.get("model") != model or rec.get("batch") != batch:
         return None, f"counter record is for {rec.get('model')} B={rec.get('batch')}"
     ratio = float(rec["traffic_bytes"]) / float(rec["alg_bytes"])
@@ -875,46 +913,61 @@ def mistral_leg(args, dev, with_cpu: bool) -> dict:
     if any(r.status.value != "decoding" for r in reqs):
         raise RuntimeError("a request finished inside the timed steps")
 
-    # ---------------- decode-attention kernel on the batch's real state
+    # ---------------- the decode step's attention launch on the batch's real state
+    # The CSR of the next decode step (each request's next position, the new
+    # token counted: its pages are allocated here as that step would), so the
+    # launch appends into the slot the next step writes anyway.
     hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
-    kv_lens = [r.current_position for r in reqs]  # tokens in the cache after the last step
-    rows = [(r.slot, r.current_position - 1) for r in reqs]
-    # rebuild the CSR for exactly these contexts (no growth: pages already held)
+    kv_lens = [r.current_position + 1 for r in reqs]
+    rows = [(r.slot, r.current_position) for r in reqs]
     sch.pt.step([], rows, B, sch.d_indptr, sch.d_indices, sch.d_last, sch.d_batch, sch.d_pos)
     w = sch.decode_wrapper
     w.plan(sch.d_indptr[: B + 1], sch.d_indices, sch.d_last[:B], hq, hkv, d, 16)
-    qs = [torch.randn(B, hq, d, device=dev, dtype=torch.bfloat16) for _ in range(cfg.num_hidden_layers)]
+    L = cfg.num_hidden_layers
+    qkvs = [torch.randn(B, (hq + 2 * hkv) * d, device=dev, dtype=torch.bfloat16) for _ in range(L)]
+    qs = [torch.randn(B, hq, d, device=dev, dtype=torch.bfloat16) for _ in range(L)]
     outs = [torch.empty_like(q) for q in qs]
-    npages = [math.ceil(n / 16) for n in kv_lens]
-    alg_bytes = sum(kv_lens) * hkv * d * 2 * 2 + 2 * B * hq * d * 2 + 4 * ((B + 1) + sum(npages) + B)
-    # The 32 launches are captured once and replayed, so the events time the
-    # kernels back to back on the GPU without host launch gaps.
-    side = torch.cuda.Stream(dev)
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for _ in range(2):
-            for l in range(cfg.num_hidden_layers):
+    alg_bytes = decode_step_attn_bytes(kv_lens, hq, hkv, d)
+    plain_bytes = decode_attn_bytes(kv_lens, hq, hkv, d)
+
+    def layer_launches(fused: bool):
+        for l in range(L):
+            if fused:
+                w.run_rope_append(qkvs[l], model.cos, model.sin, sch.kv.kv_data[l], out=outs[l])
+            else:
                 w.run(qs[l], sch.kv.kv_data[l], out=outs[l])
-    torch.cuda.current_stream().wait_stream(side)
-    attn_graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(attn_graph):
-        for l in range(cfg.num_hidden_layers):
-            w.run(qs[l], sch.kv.kv_data[l], out=outs[l])
-    attn_graph.replay()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(args.attn_iters):
-        attn_graph.replay()
-    e1.record(stream)
-    e1.synchronize()
-    launches = args.attn_iters * cfg.num_hidden_layers
-    attn_us = e0.elapsed_time(e1) * 1000 / launches
+
+    def graph_us(fused: bool) -> float:
+        """The L launches captured once and replayed, so the events time the
+        kernels back to back on the GPU without host launch gaps."""
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                layer_launches(fused)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            layer_launches(fused)
+        graph.replay()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.attn_iters):
+            graph.replay()
+        e1.record(stream)
+        e1.synchronize()
+        del graph
+        return e0.elapsed_time(e1) * 1000 / (args.attn_iters * L)
+
+    attn_us = graph_us(True)
     achieved = alg_bytes / (attn_us * 1e-6) / 1e9
-    log(f"decode attention: {attn_us:.2f} us/launch, {achieved:.0f} GB/s "
-        f"({100 * achieved / PEAK_HBM_GBPS:.1f}% of {PEAK_HBM_GBPS:.0f}), {alg_bytes / 1e6:.1f} MB/launch")
-    del attn_graph
+    plain_us = graph_us(False)
+    plain_gbps = plain_bytes / (plain_us * 1e-6) / 1e9
+    log(f"decode step attention launch (RoPE + append + attention): {attn_us:.2f} us/launch, {achieved:.0f} GB/s "
+        f"({100 * achieved / PEAK_HBM_GBPS:.1f}% of {PEAK_HBM_GBPS:.0f}), {alg_bytes / 1e6:.1f} MB/launch; "
+        f"attention alone {plain_us:.2f} us, {100 * plain_gbps / PEAK_HBM_GBPS:.1f}%")
 
     # ---------------- CPU baseline: the oracle continues this batch on the host cores
     cpu = cpu_legs = None
@@ -929,7 +982,7 @@ def mistral_leg(args, dev, with_cpu: bool) -> dict:
                          f"untimed step: {mist['step_s']} s per step",
                **{k: info[k] for k in ("os_cpu_count", "affinity_cpus", "cgroup_quota_cpus", "omp_num_threads",
                                        "threads")}}
-        layer = cpu_attn_layer_leg(sch, qs[0], alg_bytes)
+        layer = cpu_attn_layer_leg(sch, qs[0], plain_bytes)
         cpu_legs = {"mistral_attn_one_layer": {**layer, "kind": "port",
                                                "what": "oracle gather-based paged decode attention, layer 0 of "
                                                        "this batch, median after 3 warm-ups"}}
@@ -944,7 +997,7 @@ def mistral_leg(args, dev, with_cpu: bool) -> dict:
     log(f"decode, one step per round trip: {toks_single:.0f} tok/s, {single * 1000 / args.steps:.3f} ms/step")
 
     mean_ctx = round(sum(kv_lens) / B, 1)
-    traffic, basis = measured_traffic(args.model, B, mean_ctx, alg_bytes)
+    traffic, basis = measured_traffic("decode_step_attention", args.model, B, mean_ctx, alg_bytes)
     return {
         "value": round(toks, 2), "ms_per_step": round(ms_step, 4),
         "config": {"workload": f"{args.model} decode, B={B}, prompts U[128,1024] seed {args.seed}, "
@@ -953,9 +1006,15 @@ def mistral_leg(args, dev, with_cpu: bool) -> dict:
                    "batch": B, "mean_context": mean_ctx, "decode_window": args.decode_window,
                    "parallelism": "single GPU"},
         "decode_tok_s_one_step_per_round_trip": round(toks_single, 2),
+        "decode_attn_kernel": "the decode step's attention launch: RoPE of q and k, the new K/V appended, "
+                              "split-K paged attention (mi_decode_rope_append_run, decode_run_kernel<128, 4, 2, "
+                              "true>)",
         "decode_attn_us": round(attn_us, 3),
         "decode_attn_gbps": round(achieved, 1),
         "decode_attn_alg_bytes": alg_bytes,
+        "decode_attn_alone": {"us": round(plain_us, 3), "gbps": round(plain_gbps, 1), "alg_bytes": plain_bytes,
+                              "frac": round(plain_gbps / PEAK_HBM_GBPS, 4),
+                              "what": "attention alone on the same CSR (mi_decode_run, q already rotated)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBPS, 4),
                      "traffic": round(traffic) if traffic is not None else None, "traffic_basis": basis},

@@ -127,6 +127,34 @@ int mi_decode_run(void* workspace, size_t workspace_bytes, const void* q, int64_
                   int32_t num_kv_heads, int32_t head_dim, int32_t page_size, float sm_scale,
                   int32_t max_units, mi_stream_t stream);
 
+/* Decode attention with the step's RoPE and K/V append in the same launch:
+ * the three per-layer calls of the reference's decode step -- apply_rotary_emb
+ * on q and k (model.py:92-107, called at 169-170), append_paged_kv_cache
+ * (model.py:203-216) and the decode wrapper's run (model.py:235) -- for a
+ * batch that appends exactly one token per request at its last position
+ * (kv_len - 1, the decode step: scheduler.py:862-879), after mi_decode_plan
+ * of the CSR that already counts that token.  qkv: [batch] rows of bf16, row
+ * stride qkv_stride_token elements, each row num_qo_heads q heads, then
+ * num_kv_heads k heads, then num_kv_heads v heads (head_dim contiguous each).
+ * Request b's q heads and its k heads are rotated with row kv_len_b - 1 --
+ * the decode position, which the reference's RoPE takes from position_ids
+ * (model.py:399-400) -- clamped to [0, table_rows), of cos_table / sin_table,
+ * with the bf16 arithmetic of mi_rope_append; rotated k and v are written to
+ * the slot (last_page_len[b] - 1) of the request's last page, and the
+ * attention output goes to out as mi_decode_run writes it.  Pool contents and
+ * output are bit-identical to mi_rope_append (with batch_indices = b,
+ * positions = rope positions = kv_len - 1) followed by mi_decode_run on the
+ * rotated q; q is not written back.  Same shapes, workspace and plan rules as
+ * mi_decode_run. */
+int mi_decode_rope_append_run(void* workspace, size_t workspace_bytes, const void* qkv,
+                              int64_t qkv_stride_token, const void* cos_table, const void* sin_table,
+                              int64_t table_rows,
+                              void* paged_kv_cache, int64_t num_pages, const int32_t* kv_indices,
+                              void* out, int64_t out_stride_batch, int64_t out_stride_head,
+                              int32_t batch_size, int32_t num_qo_heads, int32_t num_kv_heads,
+                              int32_t head_dim, int32_t page_size, float sm_scale, int32_t max_units,
+                              mi_stream_t stream);
+
 /* ------------------------------------------------------------------------ *
  * Decode attention with no caller workspace.
  * No counterpart in the reference: for callers that cannot allocate device

@@ -53,6 +53,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _c_sz, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i32, _c_i32,
          _c_i32, _c_i32, _c_i32, _c_f32, _c_i32, _vp],
     ),
+    "mi_decode_rope_append_run": (
+        ctypes.c_int,
+        [_vp, _c_sz, _vp, _c_i64, _vp, _vp, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i32,
+         _c_i32, _c_i32, _c_i32, _c_i32, _c_f32, _c_i32, _vp],
+    ),
     "mi_decode_static_capacity": (_c_sz, []),
     "mi_decode_static": (
         ctypes.c_int,

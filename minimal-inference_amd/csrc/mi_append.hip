@@ -83,11 +83,9 @@ __global__ __launch_bounds__(256) void append_kernel(AppendParams p) {
 //
 // Replaces, per layer, the reference's apply_rotary_emb on q and k
 // (model.py:92-107, called at model.py:169-170) followed by the append
-// (model.py:203-216).  The arithmetic is the reference's bf16 composition
-// x * cos + rotate_half(x) * sin with cos / sin already in bf16
-// (server.py:251): each product is exact in fp32 and rounded to bf16, their
-// sum is taken in fp32 and rounded to bf16 -- what the three bf16 torch ops
-// do -- so the result is bit-identical to the unfused ops.
+// (model.py:203-216).  The arithmetic is mi::rope8: the reference's bf16
+// composition x * cos + rotate_half(x) * sin with cos / sin already in bf16
+// (server.py:251), bit-identical to the unfused ops.
 //
 // Work units per token: (H_q + H_kv) heads x D/16 rotate units (8 pairs
 // (j, j + D/2) each: one 16-byte load from each half) and H_kv x D/8 copy
@@ -112,34 +110,6 @@ struct RopeAppendParams {
   const int32_t* indptr;
   int32_t batch_size, num_qo_heads, num_kv_heads, head_dim, page_size;
 };
-
-__device__ __forceinline__ float lo16(uint32_t w) { return mi::bf16_lo(w); }
-__device__ __forceinline__ float hi16(uint32_t w) { return mi::bf16_hi(w); }
-
-// out_lo = x1 * c1 + (-x2) * s1, out_hi = x2 * c2 + x1 * s2, 8 lanes each:
-// each product is exact in fp32 (8-bit x 8-bit mantissas) and rounded to
-// bf16, the sum is taken in fp32 and rounded to bf16 (round to nearest even,
-// two values per v_cvt_pk_bf16_f32)
-__device__ __forceinline__ void rope8(uint4 x1, uint4 x2, uint4 c1, uint4 s1, uint4 c2, uint4 s2, uint4& o1,
-                                      uint4& o2) {
-  const uint32_t* a = &x1.x;
-  const uint32_t* b = &x2.x;
-  const uint32_t* ca = &c1.x;
-  const uint32_t* sa = &s1.x;
-  const uint32_t* cb = &c2.x;
-  const uint32_t* sb = &s2.x;
-  uint32_t* oa = &o1.x;
-  uint32_t* ob = &o2.x;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const uint32_t ac = mi::cvt_pk_bf16(lo16(a[w]) * lo16(ca[w]), hi16(a[w]) * hi16(ca[w]));
-    const uint32_t bs = mi::cvt_pk_bf16(-lo16(b[w]) * lo16(sa[w]), -hi16(b[w]) * hi16(sa[w]));
-    oa[w] = mi::cvt_pk_bf16(lo16(ac) + lo16(bs), hi16(ac) + hi16(bs));
-    const uint32_t bc = mi::cvt_pk_bf16(lo16(b[w]) * lo16(cb[w]), hi16(b[w]) * hi16(cb[w]));
-    const uint32_t as = mi::cvt_pk_bf16(lo16(a[w]) * lo16(sb[w]), hi16(a[w]) * hi16(sb[w]));
-    ob[w] = mi::cvt_pk_bf16(lo16(bc) + lo16(as), hi16(bc) + hi16(as));
-  }
-}
 
 // One workgroup per token (grid-stride over tokens): the RoPE row and the
 // slot are looked up once per token with scalar loads; the threads rotate
@@ -168,7 +138,7 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams p) {
       const int c = (u - h * upr) * 8;
       const uint16_t* src = row + int64_t(h) * d;
       uint4 o1, o2;
-      rope8(mi::load16_nt(src + c), mi::load16_nt(src + half + c), mi::load16(cs + c), mi::load16(sn + c),
+      mi::rope8(mi::load16_nt(src + c), mi::load16_nt(src + half + c), mi::load16(cs + c), mi::load16(sn + c),
             mi::load16(cs + half + c), mi::load16(sn + half + c), o1, o2);
       uint16_t* dst = p.q_out + i * p.qo_stride_tok + int64_t(h) * p.qo_stride_head;
       mi::store16(dst + c, o1);
@@ -186,7 +156,7 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams p) {
         const int c = (u - h * upr) * 8;
         const uint16_t* src = row + int64_t(h) * d;
         uint4 o1, o2;
-        rope8(mi::load16_nt(src + c), mi::load16_nt(src + half + c), mi::load16(cs + c), mi::load16(sn + c),
+        mi::rope8(mi::load16_nt(src + c), mi::load16_nt(src + half + c), mi::load16(cs + c), mi::load16(sn + c),
               mi::load16(cs + half + c), mi::load16(sn + half + c), o1, o2);
         uint16_t* dst = slot + int64_t(h - p.num_qo_heads) * d;
         mi::store16(dst + c, o1);

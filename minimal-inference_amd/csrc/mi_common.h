@@ -130,4 +130,32 @@ __device__ __forceinline__ void store16(void* p, uint4 v) { *reinterpret_cast<ui
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// ---------------------------------------------------------------- RoPE
+// Rotate-half RoPE of 8 element pairs (d, d + D/2) with bf16 cos / sin, the
+// reference's bf16 composition x * cos + rotate_half(x) * sin (model.py:
+// 92-107): out_lo = x1 * c1 + (-x2) * s1, out_hi = x2 * c2 + x1 * s2, where
+// each product is exact in fp32 (8-bit x 8-bit mantissas) and rounded to
+// bf16 and the sum is taken in fp32 and rounded to bf16 -- what the three
+// bf16 torch ops do -- so results are bit-identical to the unfused ops.
+__device__ __forceinline__ void rope8(uint4 x1, uint4 x2, uint4 c1, uint4 s1, uint4 c2, uint4 s2, uint4& o1,
+                                      uint4& o2) {
+  const uint32_t* a = &x1.x;
+  const uint32_t* b = &x2.x;
+  const uint32_t* ca = &c1.x;
+  const uint32_t* sa = &s1.x;
+  const uint32_t* cb = &c2.x;
+  const uint32_t* sb = &s2.x;
+  uint32_t* oa = &o1.x;
+  uint32_t* ob = &o2.x;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t ac = cvt_pk_bf16(bf16_lo(a[w]) * bf16_lo(ca[w]), bf16_hi(a[w]) * bf16_hi(ca[w]));
+    const uint32_t bs = cvt_pk_bf16(-bf16_lo(b[w]) * bf16_lo(sa[w]), -bf16_hi(b[w]) * bf16_hi(sa[w]));
+    oa[w] = cvt_pk_bf16(bf16_lo(ac) + bf16_lo(bs), bf16_hi(ac) + bf16_hi(bs));
+    const uint32_t bc = cvt_pk_bf16(bf16_lo(b[w]) * bf16_lo(cb[w]), bf16_hi(b[w]) * bf16_hi(cb[w]));
+    const uint32_t as = cvt_pk_bf16(bf16_lo(a[w]) * bf16_lo(sb[w]), bf16_hi(a[w]) * bf16_hi(sb[w]));
+    ob[w] = cvt_pk_bf16(bf16_lo(bc) + bf16_lo(as), bf16_hi(bc) + bf16_hi(as));
+  }
+}
+
 }  // namespace mi

@@ -121,6 +121,7 @@ struct DecodeTraits {
   static constexpr int LPI = CPR / 4;    // 16-byte loads per lane per page, for K and for V
   static constexpr int RS = D * 2 + MI_DECODE_RS_PAD;  // LDS row stride in bytes (the pad spreads the banks)
   static constexpr int SLOT = 4 * kPageSize * RS;  // two pages of K and V in LDS
+  static constexpr int RX = 4 * D * 2;  // RoPE + append form: cos, sin, new K, new V rows of a wave
   // Pages in flight per wave (~128-160 registers of staging).
   static constexpr int NB = (D == 64) ? MI_DECODE_NB64 : (D == 128) ? MI_DECODE_NB128 : 2;
   static_assert(G >= 1 && G <= 16, "group size");
@@ -135,9 +136,9 @@ struct RunParams {
   float* pml;    // per (unit, head): m, l
   uint16_t* po;  // per (unit, head): bf16 partial O row
   int pml_bytes, po_bytes;
-  const uint16_t* q;
+  const uint16_t* q;  // q rows; with RoPE the fused qkv rows (q heads first)
   int64_t q_sb, q_sh;
-  const char* pool;
+  char* pool;  // written only by the RoPE + append form
   int64_t num_pages;
   const int32_t* indices;
   uint16_t* out;
@@ -145,6 +146,12 @@ struct RunParams {
   int hkv;
   int max_items;
   float scale_log2;
+  // RoPE + append form: the cos / sin tables and the byte offset of K head 0
+  // in a qkv row (V head 0 follows the K heads)
+  const uint16_t* cos;
+  const uint16_t* sin;
+  int table_rows;
+  int k_col_bytes;
 };
 
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
@@ -429,8 +436,16 @@ __device__ __forceinline__ void publish_merge(const RunParams& p, int u, int b, 
 //                accumulator each lane already holds, and V comes from the
 //                LDS transpose read (lane (g, j) gets V[4g..4g+3][16t + j]);
 //                O[head 4g+i][16t + j] accumulates in registers.
-template <int D, int G, int W, int NB>
-__device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, lds_t* wg_lds) {
+//
+// With ROPE (mi_decode_rope_append_run) the q rows are the fused qkv rows:
+// every unit rotates its q heads with the request's cos / sin row, and the
+// unit holding the request's last page (the last split) also rotates its KV
+// head's new K row, takes the V row, stages both in LDS in place of the
+// pool's stale slot and writes them to the slot -- the decode step's RoPE
+// (model.py:169-170) and append (model.py:203-216) done by the attention
+// launch (model.py:235) with the same bf16 arithmetic as rope_append_kernel.
+template <int D, int G, int W, int NB, bool ROPE>
+__device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, lds_t* wg_lds, lds_t* rx) {
   using T = DecodeTraits<D, G>;
   using Regs = PageRegs<D, G>;
   static_assert((NB - 1) * 2 * T::LPI <= 63 && NB % 2 == 0, "vmcnt range; pages are consumed in pairs");
@@ -457,6 +472,38 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
 #pragma unroll
     for (int s = 0; s < T::KSTEPS; ++s)
       qb[s] = __builtin_bit_cast(mi::bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(rq, qoff, s * 64, 0));
+  }
+  // RoPE + append: the loads go out with Q's, before the page loads, and are
+  // used after the first pages are issued.  Lane l < D/8 loads chunk l of
+  // the cos row, the next D/8 lanes the sin row, for the wave's LDS copy
+  // (`rx`: cos, sin, new K, new V rows), from which the rotations read; the
+  // q chunks of lane (g, j) are g + 4 s, whose RoPE partners (d + D/2) are
+  // chunks s + KSTEPS / 2 of the same lane.  The new K row rotates in units
+  // of 8 pairs (d, d + D/2): lane l < D/16 takes d = 8 l + [0, 8); lanes 32 ..
+  // 32 + D/8 - 1 carry the V chunks.  Only the last split of a request
+  // appends (its rows load through a size-0 descriptor otherwise); lanes
+  // without a part read out of range.
+  constexpr int RK = D / 16, VC = D / 8;
+  const int split = u / p.hkv - item_base;
+  const bool appender = ROPE && split == nsplit - 1 && npg > 0;
+  u32x4_t cs_v, k_lo, k_hi, v_new;
+  int new_page = -1;
+  if constexpr (ROPE) {
+    // the decode position kv_len - 1 is the RoPE row: no load on the way
+    const int rp = min(max(mi::read_lane_i(iv, kItemKvLen) - 1, 0), p.table_rows - 1);
+    const bool is_cos = lane < VC, is_sin = lane >= VC && lane < 2 * VC;
+    const uint16_t* tab = (is_cos ? p.cos : p.sin) + int64_t(rp) * D;
+    const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc((void*)tab, (short)0, D * 2, kBufferWord3);
+    cs_v = __builtin_amdgcn_raw_buffer_load_b128(rt, is_cos ? 16 * lane : is_sin ? 16 * (lane - VC) : 0x7ffffff0, 0, 0);
+    // this head's K row and V row in the qkv row (V heads follow the K heads)
+    const char* krow = reinterpret_cast<const char*>(p.q + int64_t(b) * p.q_sb) + p.k_col_bytes + hkv * D * 2;
+    const __amdgpu_buffer_rsrc_t rkv = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)krow, (short)0, appender ? (p.hkv + 1) * D * 2 : 0, kBufferWord3);
+    const int ko = lane < RK ? 16 * lane : 0x7ffffff0;
+    k_lo = __builtin_amdgcn_raw_buffer_load_b128(rkv, ko, 0, 0);
+    k_hi = __builtin_amdgcn_raw_buffer_load_b128(rkv, ko, D, 0);
+    const int vo = (lane >= 32 && lane < 32 + VC) ? p.hkv * D * 2 + 16 * (lane - 32) : 0x7ffffff0;
+    v_new = __builtin_amdgcn_raw_buffer_load_b128(rkv, vo, 0, 0);
   }
 
   // The W waves of a workgroup run heads h0 .. h0 + W - 1 of one item and
@@ -532,6 +579,50 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
       }
     }
   };
+  // RoPE + append form, at the first page pair: the cos / sin rows go to
+  // `rx`, the q heads rotate in place, and this head's new K row (rotated)
+  // and V row go to `rx`; the new row later overwrites the pool's stale row
+  // in the staging slot of its page, and is written to the pool at the end
+  auto rotate = [&]() {
+    if constexpr (ROPE) {
+      if (lane < 2 * VC) lds_store16(rx + 16 * lane, cs_v);  // cos row, then sin row
+      const lds_t* cr = rx;
+      const lds_t* sr = rx + D * 2;
+#pragma unroll
+      for (int s = 0; s < T::KSTEPS / 2; ++s) {
+        const int c1 = (g + 4 * s) * 16, c2 = (g + 4 * (s + T::KSTEPS / 2)) * 16;
+        uint4 o1, o2;
+        mi::rope8(__builtin_bit_cast(uint4, qb[s]), __builtin_bit_cast(uint4, qb[s + T::KSTEPS / 2]),
+                  __builtin_bit_cast(uint4, lds_load16(cr + c1)), __builtin_bit_cast(uint4, lds_load16(sr + c1)),
+                  __builtin_bit_cast(uint4, lds_load16(cr + c2)), __builtin_bit_cast(uint4, lds_load16(sr + c2)),
+                  o1, o2);
+        qb[s] = __builtin_bit_cast(mi::bf16x8_t, o1);
+        qb[s + T::KSTEPS / 2] = __builtin_bit_cast(mi::bf16x8_t, o2);
+      }
+      if (appender) {
+        if (lane < RK) {
+          uint4 o1, o2;
+          mi::rope8(__builtin_bit_cast(uint4, k_lo), __builtin_bit_cast(uint4, k_hi),
+                    __builtin_bit_cast(uint4, lds_load16(cr + 16 * lane)),
+                    __builtin_bit_cast(uint4, lds_load16(sr + 16 * lane)),
+                    __builtin_bit_cast(uint4, lds_load16(cr + D + 16 * lane)),
+                    __builtin_bit_cast(uint4, lds_load16(sr + D + 16 * lane)), o1, o2);
+          lds_store16(rx + 4 * D + 16 * lane, __builtin_bit_cast(u32x4_t, o1));
+          lds_store16(rx + 5 * D + 16 * lane, __builtin_bit_cast(u32x4_t, o2));
+        }
+        if (lane >= 32 && lane < 32 + VC) lds_store16(rx + 6 * D + 16 * (lane - 32), v_new);
+      }
+    }
+  };
+  // the new K / V row into row `row` of staging slot `which` of this head
+  auto inject = [&](int which, int row) {
+    if constexpr (ROPE) {
+      lds_t* kl = lds + which * 2 * kPageSize * T::RS + row * T::RS;
+      if (lane < VC) lds_store16(kl + 16 * lane, lds_load16(rx + 4 * D + 16 * lane));
+      if (lane >= 32 && lane < 32 + VC)
+        lds_store16(kl + kPageSize * T::RS + 16 * (lane - 32), lds_load16(rx + 6 * D + 16 * (lane - 32)));
+    }
+  };
   // the workgroup's waves exchange staged rows: LDS writes done, then a
   // barrier (no wait on the page loads in flight)
   auto wg_sync = [&]() {
@@ -547,10 +638,28 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
 #pragma unroll
     for (int i = 0; i < 4; ++i) sv[i] = (4 * g + i < valid) ? c[i] * p.scale_log2 : -INFINITY;
   };
-  auto consume2 = [&](const Regs& ra, int va, const Regs& rb, int vb) {
+  // `next` reloads the two staging register sets with the next pages as
+  // soon as their rows are in LDS, so the loads of the next pair are in
+  // flight while this pair is consumed (Qwen2.5-7B B=48: 25.4 -> 24.8 us,
+  // Qwen2.5-72B: 69.7 -> 68.9 us; Mistral-7B B=32 unchanged).
+  // `inj` (RoPE + append form): the slot (0 / 1) whose page holds the new
+  // token, or -1.  The injection follows the barrier, so it overwrites
+  // whatever any wave staged into that row; a wave reads only its own
+  // head's slot, so no second barrier is needed.
+  bool rot_pending = ROPE;
+  auto consume2 = [&](Regs& ra, int va, Regs& rb, int vb, int inj, auto&& next) {
     stage(ra, va, 0);
     stage(rb, vb, 1);
+    // the RoPE rotations at the first pair, once its staging registers are
+    // free (before that, the pages in flight leave no room: 217 -> 256 VGPRs
+    // and spills with group 5..8)
+    if (ROPE && rot_pending) {
+      rotate();
+      rot_pending = false;
+    }
+    next(ra, rb);
     wg_sync();
+    if (ROPE && inj >= 0) inject(inj, last_valid - 1);
     float sa[4], sb[4];
     scores(0, va, sa);
     scores(1, vb, sb);
@@ -615,14 +724,17 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
       const int valid = (g_start + k == npg - 1) ? last_valid : kPageSize;
       return page_ok(k, page_id(k), gsize) ? valid : 0;
     };
+    // the slot of the pair (k, k + 1) that holds the new token, for its appender
+    auto inj_slot = [&](int k) { return !appender ? -1 : g_start + k == npg - 1 ? 0 : g_start + k + 1 == npg - 1 ? 1 : -1; };
     const int full = gsize / NB;
     for (int it = 0; it < full; ++it) {
 #pragma unroll
       for (int s = 0; s < NB; s += 2) {
         const int k = it * NB + s;
-        consume2(buf[s], page_valid(k), buf[s + 1], page_valid(k + 1));
-        issue(buf[s], k + NB, gsize);
-        issue(buf[s + 1], k + 1 + NB, gsize);
+        consume2(buf[s], page_valid(k), buf[s + 1], page_valid(k + 1), inj_slot(k), [&](Regs& x, Regs& y) {
+                   issue(x, k + NB, gsize);
+                   issue(y, k + 1 + NB, gsize);
+                 });
       }
     }
     // the last rem (< NB) pages; a pair's second page past the group's end
@@ -631,7 +743,9 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
 #pragma unroll
     for (int s = 0; s < NB - 1; s += 2)
       if (s < rem) consume2(buf[s], page_valid(full * NB + s), buf[s + 1],
-                            s + 1 < rem ? page_valid(full * NB + s + 1) : 0);
+                            s + 1 < rem ? page_valid(full * NB + s + 1) : 0, inj_slot(full * NB + s),
+                            [](Regs&, Regs&) {});
+    if (ROPE && g_start + gsize >= npg) new_page = page_id(npg - 1 - g_start);  // the last group
     g_start += gsize;
     if (g_start >= npg) break;
     gsize = min(64, npg - g_start);
@@ -639,6 +753,23 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
     // Wait here, while only size-0 loads are outstanding, so the loop head
     // carries no pending load (the first group's Q loads stay in flight).
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  }
+
+  // ---- the append: the new K / V row from `rx` to its slot, one 16-byte
+  // chunk per lane (a page id outside the pool writes nothing)
+  if constexpr (ROPE) {
+    if (appender) {
+      const bool ok = new_page >= 0 && new_page < p.num_pages;
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(ok ? p.pool + int64_t(new_page) * page_bytes : p.pool), (short)0, ok ? page_bytes : 0,
+          kBufferWord3);
+      const int row_off = (last_valid - 1) * tok_bytes + hkv * D * 2;
+      const bool kl = lane < VC, vl = lane >= 32 && lane < 32 + VC;
+      const int c = kl ? lane : lane - 32;
+      const u32x4_t x = lds_load16(rx + (kl ? 4 * D : 6 * D) + 16 * (c & (VC - 1)));
+      __builtin_amdgcn_raw_buffer_store_b128(x, rs, kl ? row_off + 16 * c : vl ? kv_bytes + row_off + 16 * c : 0x7ffffff0,
+                                             0, 0);
+    }
   }
 
   // ---- per-head denominators; O rows are heads 4g + i
@@ -671,18 +802,20 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
 // head_dim <= 128: registers capped at 256 per wave, so at least two waves
 // share a SIMD (the plan's 6 units per CU fit).  head_dim 256 needs the full
 // register file.
-template <int D, int G, int W>
+template <int D, int G, int W, bool ROPE>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 128 ? MI_DECODE_WAVES : 1))) void decode_run_kernel(
     RunParams p) {
-  __shared__ __attribute__((aligned(16))) char slot[W * DecodeTraits<D, G>::SLOT];
+  using T = DecodeTraits<D, G>;
+  __shared__ __attribute__((aligned(16))) char slot[W * T::SLOT + (ROPE ? W * T::RX : 0)];
   lds_t* lds = (lds_t*)slot;
+  lds_t* rx = lds + W * T::SLOT + (ROPE ? int(threadIdx.x >> 6) * T::RX : 0);  // this wave's RoPE rows
   int u = int(blockIdx.x) * W + int(threadIdx.x >> 6);
   // The first item is read before the unit count is known (in bounds either
   // way), so the reads are in flight together.
   int iv = load_item_word(p, u);
   const int num_units = p.header->num_units;
   while (u < num_units) {
-    decode_unit<D, G, W, DecodeTraits<D, G>::NB>(p, u, iv, lds);
+    decode_unit<D, G, W, T::NB, ROPE>(p, u, iv, lds, rx);
     u += int(gridDim.x) * W;
     if (u < num_units) iv = load_item_word(p, u);
   }
@@ -690,17 +823,17 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 128
 
 typedef void (*RunKernel)(RunParams);
 
-template <int D, int W>
+template <int D, int W, bool ROPE>
 RunKernel pick_group(int g) {
   switch (g) {
-    case 1: return decode_run_kernel<D, 1, W>;
-    case 2: return decode_run_kernel<D, 2, W>;
-    case 3: return decode_run_kernel<D, 3, W>;
-    case 4: return decode_run_kernel<D, 4, W>;
-    case 5: return decode_run_kernel<D, 5, W>;
-    case 6: return decode_run_kernel<D, 6, W>;
-    case 7: return decode_run_kernel<D, 7, W>;
-    case 8: return decode_run_kernel<D, 8, W>;
+    case 1: return decode_run_kernel<D, 1, W, ROPE>;
+    case 2: return decode_run_kernel<D, 2, W, ROPE>;
+    case 3: return decode_run_kernel<D, 3, W, ROPE>;
+    case 4: return decode_run_kernel<D, 4, W, ROPE>;
+    case 5: return decode_run_kernel<D, 5, W, ROPE>;
+    case 6: return decode_run_kernel<D, 6, W, ROPE>;
+    case 7: return decode_run_kernel<D, 7, W, ROPE>;
+    case 8: return decode_run_kernel<D, 8, W, ROPE>;
     default: return nullptr;
   }
 }
@@ -709,11 +842,12 @@ RunKernel pick_group(int g) {
 // head is short (head_dim <= 128), else one.
 int waves_per_group(int head_dim, int hkv) { return (head_dim <= 128 && hkv % 2 == 0) ? 2 : 1; }
 
+template <bool ROPE>
 RunKernel pick_kernel(int head_dim, int group, int waves) {
   switch (head_dim) {
-    case 64: return waves == 2 ? pick_group<64, 2>(group) : pick_group<64, 1>(group);
-    case 128: return waves == 2 ? pick_group<128, 2>(group) : pick_group<128, 1>(group);
-    case 256: return waves == 1 ? pick_group<256, 1>(group) : nullptr;
+    case 64: return waves == 2 ? pick_group<64, 2, ROPE>(group) : pick_group<64, 1, ROPE>(group);
+    case 128: return waves == 2 ? pick_group<128, 2, ROPE>(group) : pick_group<128, 1, ROPE>(group);
+    case 256: return waves == 1 ? pick_group<256, 1, ROPE>(group) : nullptr;
     default: return nullptr;
   }
 }
@@ -729,7 +863,7 @@ int check_shape(const char* who, int batch, int hq, int hkv, int head_dim, int p
     return mi::fail(MI_ERR_INVALID, "%s: num_qo_heads %d not a multiple of num_kv_heads %d", who, hq, hkv);
   if (page_size != kPageSize)
     return mi::fail(MI_ERR_UNSUPPORTED, "%s: page_size %d (built for 16)", who, page_size);
-  if (!pick_kernel(head_dim, hq / hkv, waves_per_group(head_dim, hkv)))
+  if (!pick_kernel<false>(head_dim, hq / hkv, waves_per_group(head_dim, hkv)))
     return mi::fail(MI_ERR_UNSUPPORTED, "%s: head_dim %d / group %d not built (head_dim 64/128/256, group 1..8)",
                     who, head_dim, hq / hkv);
   return MI_OK;
@@ -792,27 +926,26 @@ extern "C" int mi_decode_plan(void* workspace, size_t workspace_bytes, const int
   return mi::check_launch("decode_plan_kernel");
 }
 
-extern "C" int mi_decode_run(void* workspace, size_t workspace_bytes, const void* q,
-                             int64_t q_stride_batch, int64_t q_stride_head, const void* paged_kv_cache,
-                             int64_t num_pages, const int32_t* kv_indices, void* out,
-                             int64_t out_stride_batch, int64_t out_stride_head, int32_t batch_size,
-                             int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
-                             int32_t page_size, float sm_scale, int32_t max_units, mi_stream_t stream) {
-  mi::clear_error();
-  int rc = check_shape("decode run", batch_size, num_qo_heads, num_kv_heads, head_dim, page_size);
+namespace {
+
+// The run launch shared by the plain and the RoPE + append forms: checks the
+// workspace and arguments, fills what the kernel reads of a plan, launches.
+// `rp` arrives with the q / pool / out / RoPE fields set.
+int launch_run(const char* who, bool rope, RunParams rp, void* workspace, size_t workspace_bytes, int32_t batch_size,
+               int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size, float sm_scale,
+               int32_t max_units, mi_stream_t stream) {
+  int rc = check_shape(who, batch_size, num_qo_heads, num_kv_heads, head_dim, page_size);
   if (rc) return rc;
   if (batch_size == 0) return MI_OK;
   if (max_units <= 0) max_units = units_that_fit(workspace_bytes, batch_size, num_qo_heads, num_kv_heads, head_dim);
   const DecodeLayout L = decode_layout(batch_size, num_qo_heads, num_kv_heads, head_dim, max_units);
   if (!workspace || workspace_bytes < L.total)
-    return mi::fail(MI_ERR_WORKSPACE, "decode run: workspace %zu bytes, need %zu", workspace_bytes, L.total);
-  if (!q || !paged_kv_cache || !kv_indices || !out)
-    return mi::fail(MI_ERR_INVALID, "decode run: null pointer argument");
-  if ((reinterpret_cast<uintptr_t>(q) & 15) || (reinterpret_cast<uintptr_t>(paged_kv_cache) & 15) ||
-      q_stride_batch % 8 || q_stride_head % 8)
-    return mi::fail(MI_ERR_INVALID, "decode run: q rows and pool must be 16-byte aligned");
+    return mi::fail(MI_ERR_WORKSPACE, "%s: workspace %zu bytes, need %zu", who, workspace_bytes, L.total);
+  if (!rp.q || !rp.pool || !rp.indices || !rp.out) return mi::fail(MI_ERR_INVALID, "%s: null pointer argument", who);
+  if ((reinterpret_cast<uintptr_t>(rp.q) & 15) || (reinterpret_cast<uintptr_t>(rp.pool) & 15) || rp.q_sb % 8 ||
+      rp.q_sh % 8)
+    return mi::fail(MI_ERR_INVALID, "%s: q rows and pool must be 16-byte aligned", who);
   char* ws = static_cast<char*>(workspace);
-  RunParams rp;
   rp.header = reinterpret_cast<const DecodeHeader*>(ws);
   rp.items = reinterpret_cast<const DecodeItem*>(ws + L.items);
   rp.counters = reinterpret_cast<int*>(ws + L.counters);
@@ -820,23 +953,74 @@ extern "C" int mi_decode_run(void* workspace, size_t workspace_bytes, const void
   rp.po = reinterpret_cast<uint16_t*>(ws + L.po);
   rp.pml_bytes = int(L.po - L.pml);
   rp.po_bytes = int(L.total - L.po);
-  rp.q = static_cast<const uint16_t*>(q);
-  rp.q_sb = q_stride_batch;
-  rp.q_sh = q_stride_head;
-  rp.pool = static_cast<const char*>(paged_kv_cache);
-  rp.num_pages = num_pages;
-  rp.indices = kv_indices;
-  rp.out = static_cast<uint16_t*>(out);
-  rp.o_sb = out_stride_batch;
-  rp.o_sh = out_stride_head;
   rp.hkv = num_kv_heads;
   rp.max_items = L.max_items;
   const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf(float(head_dim));
   rp.scale_log2 = scale * mi::kLog2e;
   const int waves = waves_per_group(head_dim, num_kv_heads);
-  RunKernel k = pick_kernel(head_dim, num_qo_heads / num_kv_heads, waves);
+  RunKernel k = rope ? pick_kernel<true>(head_dim, num_qo_heads / num_kv_heads, waves)
+                     : pick_kernel<false>(head_dim, num_qo_heads / num_kv_heads, waves);
   hipLaunchKernelGGL(k, dim3(run_grid(max_units, waves)), dim3(64 * waves), 0, static_cast<hipStream_t>(stream), rp);
   return mi::check_launch("decode_run_kernel");
+}
+
+}  // namespace
+
+extern "C" int mi_decode_run(void* workspace, size_t workspace_bytes, const void* q,
+                             int64_t q_stride_batch, int64_t q_stride_head, const void* paged_kv_cache,
+                             int64_t num_pages, const int32_t* kv_indices, void* out,
+                             int64_t out_stride_batch, int64_t out_stride_head, int32_t batch_size,
+                             int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                             int32_t page_size, float sm_scale, int32_t max_units, mi_stream_t stream) {
+  mi::clear_error();
+  RunParams rp = {};
+  rp.q = static_cast<const uint16_t*>(q);
+  rp.q_sb = q_stride_batch;
+  rp.q_sh = q_stride_head;
+  rp.pool = static_cast<char*>(const_cast<void*>(paged_kv_cache));  // read only in this form
+  rp.num_pages = num_pages;
+  rp.indices = kv_indices;
+  rp.out = static_cast<uint16_t*>(out);
+  rp.o_sb = out_stride_batch;
+  rp.o_sh = out_stride_head;
+  return launch_run("decode run", false, rp, workspace, workspace_bytes, batch_size, num_qo_heads, num_kv_heads,
+                    head_dim, page_size, sm_scale, max_units, stream);
+}
+
+extern "C" int mi_decode_rope_append_run(void* workspace, size_t workspace_bytes, const void* qkv,
+                                         int64_t qkv_stride_token, const void* cos_table, const void* sin_table,
+                                         int64_t table_rows,
+                                         void* paged_kv_cache, int64_t num_pages, const int32_t* kv_indices,
+                                         void* out, int64_t out_stride_batch, int64_t out_stride_head,
+                                         int32_t batch_size, int32_t num_qo_heads, int32_t num_kv_heads,
+                                         int32_t head_dim, int32_t page_size, float sm_scale, int32_t max_units,
+                                         mi_stream_t stream) {
+  mi::clear_error();
+  if (batch_size > 0 && (!cos_table || !sin_table))
+    return mi::fail(MI_ERR_INVALID, "decode rope append run: null RoPE table");
+  if (table_rows <= 0 || table_rows > (int64_t(1) << 30))
+    return mi::fail(MI_ERR_INVALID, "decode rope append run: table_rows %lld", (long long)table_rows);
+  if ((reinterpret_cast<uintptr_t>(cos_table) & 15) || (reinterpret_cast<uintptr_t>(sin_table) & 15))
+    return mi::fail(MI_ERR_INVALID, "decode rope append run: cos / sin tables must be 16-byte aligned");
+  if (num_kv_heads > 0 && qkv_stride_token < int64_t(num_qo_heads + 2 * num_kv_heads) * head_dim)
+    return mi::fail(MI_ERR_INVALID, "decode rope append run: qkv row stride %lld shorter than (Hq + 2 Hkv) * D",
+                    (long long)qkv_stride_token);
+  RunParams rp = {};
+  rp.q = static_cast<const uint16_t*>(qkv);
+  rp.q_sb = qkv_stride_token;
+  rp.q_sh = head_dim;
+  rp.pool = static_cast<char*>(paged_kv_cache);
+  rp.num_pages = num_pages;
+  rp.indices = kv_indices;
+  rp.out = static_cast<uint16_t*>(out);
+  rp.o_sb = out_stride_batch;
+  rp.o_sh = out_stride_head;
+  rp.cos = static_cast<const uint16_t*>(cos_table);
+  rp.sin = static_cast<const uint16_t*>(sin_table);
+  rp.table_rows = int(table_rows);
+  rp.k_col_bytes = num_qo_heads * head_dim * 2;
+  return launch_run("decode rope append run", true, rp, workspace, workspace_bytes, batch_size, num_qo_heads,
+                    num_kv_heads, head_dim, page_size, sm_scale, max_units, stream);
 }
 
 // ------------------------------------------------------------------ no caller workspace

@@ -44,11 +44,12 @@ struct alignas(128) DecodeItem {
   int split;
   int nsplit;
   int item_base;  // item index of split 0 of this request
-  int pad;
+  int kv_len;     // the request's tokens (its decode position + 1)
 };
 static_assert(sizeof(DecodeItem) == 128, "item is read as 32 lanes x 4 bytes");
 constexpr int kItemB = kInlinePages, kItemBegin = kInlinePages + 1, kItemEnd = kInlinePages + 2,
-              kItemLast = kInlinePages + 3, kItemNsplit = kInlinePages + 5, kItemBase = kInlinePages + 6;
+              kItemLast = kInlinePages + 3, kItemNsplit = kInlinePages + 5, kItemBase = kInlinePages + 6,
+              kItemKvLen = kInlinePages + 7;
 
 // error: 1 = a request's items did not fit the workspace (its rows are not
 // computed); 2 = the page-table step that should have laid out the batch
@@ -267,7 +268,7 @@ __device__ inline void write_item(const PlanParams& p, int idx, const int* scan,
   it.split = sp;
   it.nsplit = nsr;
   it.item_base = first;
-  it.pad = 0;
+  it.kv_len = (npr == 0) ? 0 : (npr - 1) * kPageSize + s_lpl[r];
   // all kInlinePages loads issued together from in-range positions (clamped
   // to the item's last page), the ones past the end dropped after
   if (it.page_end > it.page_begin) {

@@ -133,3 +133,51 @@ class BatchDecodeWithPagedKVCacheWrapper:
         return out
 
     forward = run
+
+    def run_rope_append(self, qkv: torch.Tensor, cos_cache: torch.Tensor, sin_cache: torch.Tensor,
+                        paged_kv_cache: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
+        """The decode step's RoPE, K/V append and attention in one launch.
+
+        Stands for ``rope_append_paged_kv_cache`` (the reference's RoPE on q
+        and k, model.py:169-170, and ``append_paged_kv_cache``,
+        model.py:203-216) followed by ``run`` (model.py:235) when every
+        request of the plan appends exactly one token at its last position
+        (position kv_len - 1, as in decode): ``qkv`` is ``[B, (Hq + 2 Hkv) *
+        D]`` (q heads, k heads, v heads), request b is rotated with row
+        kv_len_b - 1 (its decode position) of the bf16 ``[rows, D]`` tables,
+        its rotated k and v go to slot ``last_page_len[b] - 1`` of its last
+        page, and the result is the attention output ``[B, Hq, D]``.  Pool and
+        output are bit-identical to the three-call sequence with rope positions
+        kv_len - 1; ``qkv`` is not modified.
+        """
+        if not self._planned:
+            raise RuntimeError("run_rope_append() called before plan()")
+        num_pages, page_size, hkv, d = require_pool("paged_kv_cache", paged_kv_cache)
+        if (page_size, hkv, d) != (self._ps, self._hkv, self._d):
+            raise ValueError(f"pool geometry {(page_size, hkv, d)} differs from plan "
+                             f"{(self._ps, self._hkv, self._d)}")
+        require_gpu("qkv", qkv)
+        if qkv.dtype != torch.bfloat16 or qkv.dim() != 2 or qkv.stride(1) != 1:
+            raise ValueError("qkv must be a [B, (Hq + 2 Hkv) * D] bf16 tensor with contiguous rows")
+        if qkv.shape != (self._batch, (self._hq + 2 * self._hkv) * d):
+            raise ValueError(f"qkv is {tuple(qkv.shape)}, the plan needs "
+                             f"({self._batch}, {(self._hq + 2 * self._hkv) * d})")
+        for name, tab in (("cos_cache", cos_cache), ("sin_cache", sin_cache)):
+            require_gpu(name, tab)
+            if tab.dtype != torch.bfloat16 or tab.dim() != 2 or tab.shape[1] != d or not tab.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous [rows, {d}] bf16 table")
+        if cos_cache.shape != sin_cache.shape:
+            raise ValueError("cos_cache and sin_cache differ in shape")
+        if out is None:
+            out = torch.empty(self._batch, self._hq, d, dtype=qkv.dtype, device=qkv.device)
+        else:
+            require_rows("out", out, self._hq, d)
+            if out.shape[0] != self._batch:
+                raise ValueError("out batch differs from the plan")
+        _lib.call(
+            "mi_decode_rope_append_run", self._ws.data_ptr(), self._ws_bytes, qkv.data_ptr(), qkv.stride(0),
+            cos_cache.data_ptr(), sin_cache.data_ptr(), cos_cache.shape[0],
+            paged_kv_cache.data_ptr(), num_pages, self._indices.data_ptr(), out.data_ptr(), out.stride(0),
+            out.stride(1), self._batch, self._hq, self._hkv, d, self._ps, self._scale, 0, stream_of(qkv),
+        )
+        return out

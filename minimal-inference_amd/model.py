@@ -13,7 +13,10 @@ form): q/k/v projections are one fused GEMM and gate/up one fused GEMM, and
 prefill computes logits only for each request's last position.  By default
 RoPE on q and k and the K/V append run as one HIP launch
 (``rope_append_paged_kv_cache``), bit-identical to the reference's bf16
-RoPE ops followed by the append; ``fused_rope=False`` keeps the separate ops.
+RoPE ops followed by the append, and in decode steps the attention launch
+does both itself (``run_rope_append``; ``fused_decode=False`` keeps the
+separate launch), bit-identical again; ``fused_rope=False`` keeps the
+separate ops.
 By default the residual adds and the RMSNorms that follow them run as one
 HIP kernel each, and SiLU(gate) * up as one (``dense.add_rms_norm`` /
 ``dense.silu_mul``, fp32 math, one bf16 rounding per output);
@@ -157,9 +160,10 @@ class AttentionBackend:
 
 class Model:
     def __init__(self, cfg: ModelConfig, device, dtype=torch.bfloat16, seed: int = 0, max_positions: int | None = None,
-                 fused_rope: bool = True, fused_dense: bool = True):
+                 fused_rope: bool = True, fused_dense: bool = True, fused_decode: bool = True):
         self.cfg = cfg
         self.fused_rope = fused_rope
+        self.fused_decode = fused_decode
         self.fused_dense = fused_dense
         self.device = torch.device(device)
         self.dtype = dtype
@@ -211,7 +215,11 @@ class Model:
                 h = F.rms_norm(x, (cfg.hidden_size,), L.in_norm, eps)
             qkv = F.linear(h, L.w_qkv, L.b_qkv)
             kv_data = backend.paged_kv_cache.kv_data[layer_idx]
-            if fused:
+            if fused and backend.mode == "decode" and self.fused_decode:
+                # RoPE, append and attention in one launch (one new token per
+                # request, at its last position)
+                o = backend.wrapper.run_rope_append(qkv, self.cos, self.sin, kv_data)
+            elif fused:
                 # q rotated in place in qkv's q columns; k rotated and v appended
                 q = rope_append_paged_kv_cache(qkv, nq, nkv, rope_pos, self.cos, self.sin, backend.batch_indices,
                                                backend.positions, kv_data, backend.kv_page_indices,
@@ -222,7 +230,8 @@ class Model:
                 v = qkv[:, (nq + nkv) * d:].view(t, nkv, d)
                 append_paged_kv_cache(k, v, backend.batch_indices, backend.positions, kv_data,
                                       backend.kv_page_indices, backend.kv_page_indptr, backend.kv_last_page_len)
-            o = backend.wrapper.run(q, kv_data)
+            if not (fused and backend.mode == "decode" and self.fused_decode):
+                o = backend.wrapper.run(q, kv_data)
             if not dense:
                 x = x + F.linear(o.view(t, nq * d), L.w_o)
                 h = F.rms_norm(x, (cfg.hidden_size,), L.post_norm, eps)

@@ -241,3 +241,27 @@ def test_large_batches(dev, parity, B, hq, hkv, d, max_ctx):
     lens = torch.randint(1, max_ctx + 1, (B,), generator=g).tolist()
     b = make_paged_batch(lens, hq, hkv, d, seed=B)
     parity(_decode(dev, b, hq, hkv, d), _ref(b))
+
+
+@pytest.mark.parametrize("hq,hkv,d,lo,hi", [
+    (32, 8, 128, 153, 1049),    # Mistral-7B decode batch: items of 6-7 pages
+    (64, 8, 128, 512, 4096),    # Qwen2.5-72B heads: items of 16-29 pages, some past the 24 inline page ids
+    (14, 2, 64, 512, 4096),     # Qwen2.5-0.5B heads: head_dim 64, four pages in flight
+])
+def test_repeated_runs_are_bit_identical(dev, parity, hq, hkv, d, lo, hi):
+    """Units finish in a different order on every launch and whichever split
+    of a request arrives last merges: the output must not depend on which, so
+    12 launches of one plan give bit-identical outputs, within the oracle's
+    bound.  Items of odd and even page counts, with and without page groups
+    past the inline ids, all occur here."""
+    g = torch.Generator().manual_seed(hq + lo)
+    lens = torch.exp(torch.empty(48).uniform_(math.log(lo), math.log(hi), generator=g)).round().int().tolist()
+    b = make_paged_batch(lens, hq, hkv, d, seed=hq + d)
+    pool, q, ip, ix, lp = to_dev(b, dev)
+    w = _wrapper(dev)
+    w.plan(ip, ix, lp, hq, hkv, d, 16)
+    outs = [w.run(q, pool).clone() for _ in range(12)]
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    parity(outs[0].float().cpu(), _ref(b))

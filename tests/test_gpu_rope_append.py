@@ -127,3 +127,76 @@ def test_model_forward_fused_equals_unfused(dev):
             sch.step()
         outs.append([r.generated_tokens for r in reqs])
     assert outs[0] == outs[1]
+
+
+@pytest.mark.parametrize("hq,hkv,d,theta", [(32, 8, 128, 1e6), (14, 2, 64, 1e6), (28, 4, 128, 1e6),
+                                            (64, 8, 128, 1e6), (8, 8, 256, 1e4), (12, 4, 64, 1e4),
+                                            (6, 3, 128, 1e4)])
+def test_decode_attention_with_rope_append_equals_the_three_calls(dev, parity, hq, hkv, d, theta):
+    """run_rope_append (RoPE of q and k, the K/V append and decode attention
+    in one launch) against rope_append_paged_kv_cache followed by the
+    wrapper's run on the rotated q: bit-identical output and pool, qkv left
+    unmodified; requests from 1 token (the new one alone) to 5,000 (many
+    splits, page groups past the inline ids), new tokens on the first and
+    last row of a page; the output within the oracle's bound."""
+    from minimal_inference_amd.decode import BatchDecodeWithPagedKVCacheWrapper
+    from minimal_inference_amd.page import rope_append_paged_kv_cache
+    from oracle import attention as oatt
+
+    lens = [1, 2, 16, 17, 64, 203, 511, 900, 1024, 2049, 5000, 33]
+    pages = sum(math.ceil(n / 16) for n in lens) + 8
+    pool, indptr, indices, last, qkv = _case(lens, [(b, n - 1) for b, n in enumerate(lens)], hq, hkv, d, pages,
+                                             seed=hq * 13 + d)
+    qkv = (qkv.float() / 3).to(torch.bfloat16)  # N(0, 1) rows, the scale of the other decode parity cases
+    cos, sin = orope.tables(d, 8192, theta)
+    pos = [n - 1 for n in lens]
+    i32 = lambda x: torch.tensor(x, dtype=torch.int32, device=dev)
+    cos_d, sin_d, ip, ix, lp = cos.to(dev), sin.to(dev), i32(indptr), indices.to(dev), i32(last)
+    outs, pools = [], []
+    for fused in (False, True):
+        w = BatchDecodeWithPagedKVCacheWrapper(torch.empty(128 << 20, dtype=torch.uint8, device=dev))
+        w.plan(ip, ix, lp, hq, hkv, d, 16)
+        pool_d = pool.to(dev)
+        qkv_d = qkv.to(dev)
+        if fused:
+            o = w.run_rope_append(qkv_d, cos_d, sin_d, pool_d)
+            torch.cuda.synchronize()
+            assert torch.equal(qkv_d.cpu(), qkv)
+        else:
+            q = rope_append_paged_kv_cache(qkv_d, hq, hkv, i32(pos), cos_d, sin_d, i32(list(range(len(lens)))),
+                                           i32(pos), pool_d, ix, ip, lp)
+            o = w.run(q, pool_d)
+        torch.cuda.synchronize()
+        outs.append(o.cpu())
+        pools.append(pool_d.cpu())
+    assert torch.equal(pools[1], pools[0])
+    assert torch.equal(outs[1], outs[0])
+    want_q, want_pool = orope.rope_append(qkv, hq, hkv, pos, cos, sin, pool, indptr, indices.tolist(),
+                                          list(range(len(lens))), pos)
+    assert torch.equal(pools[1], want_pool)
+    parity(outs[1].float(), oatt.decode(want_q, want_pool, indptr, indices.tolist(), last))
+
+
+def test_engine_decode_with_and_without_the_fused_launch(dev):
+    """The engine (graphs, 8 slots, padded batches) with the decode step's
+    RoPE + append inside the attention launch and with the separate launch:
+    identical greedy tokens step for step."""
+    from minimal_inference_amd.engine import Request, Scheduler
+    from minimal_inference_amd.model import PRESETS, Model
+
+    cfg = PRESETS["qwen2.5-0.5b"]
+    cfg = type(cfg)(**{**cfg.__dict__, "num_hidden_layers": 6})
+    outs = []
+    for fused_decode in (True, False):
+        model = Model(cfg, dev, seed=4, max_positions=1024, fused_decode=fused_decode)
+        sch = Scheduler(model, max_batch_size=8, max_seq_len=512, seed=4)
+        g = torch.Generator().manual_seed(9)
+        reqs = [Request(str(i), torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist(), 20, 0.0, 1.0)
+                for i, n in enumerate([9, 40, 77, 16, 1, 130])]
+        for r in reqs:
+            sch.submit(r)
+        while sch.has_work():
+            sch.step()
+        assert sch.pt.error_word() == 0
+        outs.append([r.generated_tokens for r in reqs])
+    assert outs[0] == outs[1]
