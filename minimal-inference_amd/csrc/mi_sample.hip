@@ -9,24 +9,33 @@
 //     tokens whose mass reaches top_p, ties at the boundary included.
 //
 // Each row is split into chunks of 4,096 tokens, one 256-thread workgroup
-// per (chunk, row), in two launches; the last workgroup of a row to finish a
-// launch (an agent-scope counter; partials written and read device-coherent,
-// so no workgroup ever waits for another) combines the row's chunks:
-//   pass 1: the scaled logits' 16-bit order keys; per chunk the greedy
-//     argmax, the max key and, for top-p rows, a 1,024-bin histogram of
-//     probability mass over key >> 6 (relative to the chunk's max).  The last
-//     workgroup writes a greedy row's id, or finds the row's top-p boundary
-//     bin: the bin where the mass accumulated from the top reaches top_p of
-//     the total.
-//   pass 2 (sampled rows): the exponential race (Gumbel-max):
-//     argmax_i (s_i * log2 e - log2(-log2 u_i)), which selects i with
-//     probability proportional to exp(s_i), over the tokens above the
-//     boundary bin, and for the boundary bin's 64 keys their mass and race
-//     winner per key.  The last workgroup resolves the boundary key exactly
-//     (ties at it kept) and picks the winner over the kept tokens.
+// per (chunk, row), in two launches.  Sampled rows draw by the exponential
+// race (Gumbel-max): argmax_i (s_i * log2 e - log2(-log2 u_i)) selects i with
+// probability proportional to exp(s_i).
+//   pass 1, rows without top-p: each wave's winner over its 1,024 tokens (the
+//     greedy argmax, or the race); pass 2's chunk-0 workgroup of the row
+//     takes the best of the row's wave winners.
+//   pass 1, top-p rows: the chunk's max key and a 1,024-bin histogram of
+//     probability mass over key >> 6 (relative to the chunk max) with its 32
+//     super-bin sums.  The histogram adds 2^40 fixed-point masses with 64-bit
+//     integer LDS atomics: exact, so no sum depends on the order of the
+//     additions, and several times faster than float LDS atomics on gfx950.
+//   pass 2, top-p rows: every workgroup of the row combines the chunks'
+//     super-bin sums (scaled to the row max), finds the super-bin where the
+//     mass accumulated from the top reaches top_p of the total, then the
+//     boundary bin inside it from that super-bin's 32 bins of every chunk --
+//     the same arithmetic in the same order in every workgroup, so all of
+//     them agree.  Then the race over the tokens above the boundary bin and,
+//     for the boundary bin's 64 keys, their mass and race winner per key.
+//     The row's last workgroup (an agent-scope counter; partials written and
+//     read device-coherent, so no workgroup ever waits for another) resolves
+//     the boundary key exactly (ties at it kept) and picks the winner over
+//     the kept tokens.
 // u_i comes from Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random
 // numbers: as easy as 1, 2, 3", SC 2011) with counter (token / 4, row,
-// offset) and key = seed; the last workgroup of pass 2 advances the offset.
+// offset) and key = seed.  Pass 1 reads the offset and keeps a copy in the
+// workspace; pass 2 reads the copy, so one workgroup of it can advance the
+// offset with no count of the grid's workgroups.
 #include <math.h>
 
 #include "mi_common.h"
@@ -68,21 +77,24 @@ __device__ __forceinline__ float u01(uint32_t x) { return (float(x >> 8) + 0.5f)
 constexpr int kT = 256;              // threads per workgroup
 constexpr int kGroupsPerThread = 4;  // 4-token groups per thread
 constexpr int kChunk = kT * kGroupsPerThread * 4;  // 4,096 tokens per workgroup
-constexpr int kBins = 1024;          // pass-1 bins: key >> 6
+constexpr int kBins = 1024;          // histogram bins: key >> 6
 constexpr int kSub = 64;             // keys per bin
+constexpr int kSup = 32;             // super-bins of kBins / kSup bins
+constexpr int kBinsPerSup = kBins / kSup;
+constexpr int kGrp = kT / kSup;      // thread groups of the per-row combines
 constexpr int kNW = kT / 64;
 constexpr int kMaxChunks = 256;      // vocabularies up to 1,048,576 tokens
 // 16-bit keys: the bf16 order key, with NaN (either sign) as 0xFFFF -- above
 // +inf, whose key is 0xFF80 -- and 0 marking a slot past the vocabulary (no
 // bf16 value maps to 0: -inf is 0x007F).
 constexpr uint32_t kNaN16 = 0xFFFFu;
+// Masses in [0, 1] as 2^40 fixed point: a chunk's 4,096 tokens sum to at
+// most 2^52, a row's 2^20 tokens to at most 2^60.
+constexpr float kFix = 1099511627776.0f;
+constexpr float kUnfix = 1.0f / 1099511627776.0f;
 
-struct RowInfo {
-  float smax;    // max scaled logit x log2 e
-  int bstar;     // boundary bin, -1: every token is kept
-  float above;   // mass of the bins above it (relative to the max)
-  float target;  // top_p x total mass
-};
+__device__ __forceinline__ unsigned long long to_fix(float m) { return static_cast<unsigned long long>(m * kFix); }
+__device__ __forceinline__ float from_fix(unsigned long long q) { return static_cast<float>(q) * kUnfix; }
 
 struct SampleParams {
   const uint16_t* logits;
@@ -93,121 +105,85 @@ struct SampleParams {
   uint2 seed;
   uint64_t* offset;
   int64_t* out;
-  // workspace (zero counters between calls)
-  int* cnt1;
-  int* cnt2;
-  int* done;
-  RowInfo* info;
-  uint32_t* p1_max;
-  unsigned long long* p1_arg;
-  float* p1_bins;
-  unsigned long long* p2_best;
-  float* p2_sub_mass;
-  unsigned long long* p2_sub_best;
+  // workspace: counters (zero between calls) and per-chunk partials
+  int* cnt;
+  uint64_t* off_copy;            // the draw offset as pass 1 read it
+  unsigned long long* part;      // [row][chunk][kNW] wave winners, rows without top-p
+  uint32_t* cmax;                // [row][chunk] max key, top-p rows
+  float* sup;                    // [row][chunk][kSup] super-bin mass, relative to the chunk max
+  float* bins;                   // [row][chunk][kBins] bin mass, relative to the chunk max
+  unsigned long long* best;      // [row][chunk] race winner above the boundary bin
+  unsigned long long* sub_mass;  // [row][chunk][kSub] boundary-bin key mass (fixed point, relative to the row max)
+  unsigned long long* sub_best;  // [row][chunk][kSub] boundary-bin key race winner
 };
 
-// (key, index) argmax: larger key wins, lower index breaks ties.
-__device__ __forceinline__ void better(uint32_t& bk, int& bi, uint32_t k, int i) {
-  if (k > bk || (k == bk && i < bi)) {
-    bk = k;
-    bi = i;
-  }
+// ---------------------------------------------------------------- lanes
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
+  return uint32_t(__builtin_amdgcn_update_dpp(0, int(x), CTRL, 0xf, 0xf, false));
 }
-__device__ __forceinline__ void betterf(float& bv, int& bi, float v, int i) {
-  if (v > bv || (v == bv && i < bi)) {
-    bv = v;
-    bi = i;
-  }
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long x) {
+  return (static_cast<unsigned long long>(dpp_u<CTRL>(uint32_t(x >> 32))) << 32) | dpp_u<CTRL>(uint32_t(x));
 }
 
-// (value, index) argmax across lanes without LDS: each step fetches a
-// partner's pair with a DPP or lane-swap move and keeps the better one.
-template <typename F>
-__device__ __forceinline__ void arg_take(F& bv, int& bi, uint32_t ov_bits, int oi) {
-  const F ov = __builtin_bit_cast(F, ov_bits);
-  if (ov > bv || (ov == bv && oi < bi)) {
-    bv = ov;
-    bi = oi;
-  }
-}
-template <int CTRL, typename F>
-__device__ __forceinline__ void arg_dpp(F& bv, int& bi) {
-  const uint32_t ov = uint32_t(__builtin_amdgcn_update_dpp(0, int(__builtin_bit_cast(uint32_t, bv)), CTRL, 0xf, 0xf, false));
-  const int oi = __builtin_amdgcn_update_dpp(0, bi, CTRL, 0xf, 0xf, false);
-  arg_take(bv, bi, ov, oi);
-}
-// Every lane of each aligned group of 16 ends with the group's best pair.
-template <typename F>
-__device__ __forceinline__ void group16_argmax(F& bv, int& bi) {
-  arg_dpp<mi::kDppQuadSwap1>(bv, bi);
-  arg_dpp<mi::kDppQuadSwap2>(bv, bi);
-  arg_dpp<mi::kDppRowHalfMirror>(bv, bi);
-  arg_dpp<mi::kDppRowMirror>(bv, bi);
-}
-// The swaps exchange values between lane halves; both results are taken
-// (one of them is the lane's own pair, which changes nothing).
-template <typename F>
-__device__ __forceinline__ void wave_argmax(F& bv, int& bi) {
-  group16_argmax(bv, bi);
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  x = max(x, dpp_u<mi::kDppQuadSwap1>(x));
+  x = max(x, dpp_u<mi::kDppQuadSwap2>(x));
+  x = max(x, dpp_u<mi::kDppRowHalfMirror>(x));
+  x = max(x, dpp_u<mi::kDppRowMirror>(x));
+  // the swaps exchange values between lane halves; both results are taken
+  // (one of them is the lane's own value)
   {
-    const uint32_t v = __builtin_bit_cast(uint32_t, bv);
-    const auto rv = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-    const auto ri = __builtin_amdgcn_permlane16_swap(uint32_t(bi), uint32_t(bi), false, false);
-    arg_take(bv, bi, rv[0], int(ri[0]));
-    arg_take(bv, bi, rv[1], int(ri[1]));
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    x = max(x, max(uint32_t(r[0]), uint32_t(r[1])));
   }
   {
-    const uint32_t v = __builtin_bit_cast(uint32_t, bv);
-    const auto rv = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    const auto ri = __builtin_amdgcn_permlane32_swap(uint32_t(bi), uint32_t(bi), false, false);
-    arg_take(bv, bi, rv[0], int(ri[0]));
-    arg_take(bv, bi, rv[1], int(ri[1]));
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    x = max(x, max(uint32_t(r[0]), uint32_t(r[1])));
   }
+  return x;
 }
 
-// Workgroup argmax (larger value, then lower index) over kNW waves; every
-// thread gets the result.  `lowest` ranks below every candidate.  sv / si
-// hold one pair per wave; the call starts and ends with them free.
-template <typename F, int NW = kNW>
-__device__ __forceinline__ void block_argmax(F& bv, int& bi, F* sv, int* si, F lowest) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  wave_argmax(bv, bi);
-  if (lane == 0) {
-    sv[w] = bv;
-    si[w] = bi;
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long x) {
+  x = max(x, dpp_u64<mi::kDppQuadSwap1>(x));
+  x = max(x, dpp_u64<mi::kDppQuadSwap2>(x));
+  x = max(x, dpp_u64<mi::kDppRowHalfMirror>(x));
+  x = max(x, dpp_u64<mi::kDppRowMirror>(x));
+  {
+    const uint32_t hi = uint32_t(x >> 32), lo = uint32_t(x);
+    const auto rh = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    const auto rl = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    x = max(x, (static_cast<unsigned long long>(uint32_t(rh[0])) << 32) | uint32_t(rl[0]));
+    x = max(x, (static_cast<unsigned long long>(uint32_t(rh[1])) << 32) | uint32_t(rl[1]));
   }
-  __syncthreads();
-  F v = lowest;
-  int i = 0x7fffffff;
-#pragma unroll
-  for (int k = 0; k < NW; ++k) {
-    const F ov = sv[k];
-    const int oi = si[k];
-    if (ov > v || (ov == v && oi < i)) {
-      v = ov;
-      i = oi;
-    }
+  {
+    const uint32_t hi = uint32_t(x >> 32), lo = uint32_t(x);
+    const auto rh = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    const auto rl = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    x = max(x, (static_cast<unsigned long long>(uint32_t(rh[0])) << 32) | uint32_t(rl[0]));
+    x = max(x, (static_cast<unsigned long long>(uint32_t(rh[1])) << 32) | uint32_t(rl[1]));
   }
-  bv = v;
-  bi = i;
-  __syncthreads();
+  return x;
 }
 
-template <int NW = kNW>
-__device__ __forceinline__ float block_sum(float x, float* sf) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  x = mi::wave_sum(x);
-  if (lane == 0) sf[w] = x;
+// Workgroup max; `s` holds one value per wave and is not reused by the caller
+// before its next barrier.
+template <typename U>
+__device__ __forceinline__ U block_max(U x, U* s) {
+  if constexpr (sizeof(U) == 8) x = wave_max_u64(x);
+  else x = wave_max_u32(x);
+  if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = x;
   __syncthreads();
-  float s = 0.f;
+  U r = s[0];
 #pragma unroll
-  for (int k = 0; k < NW; ++k) s += sf[k];
-  __syncthreads();
-  return s;
+  for (int k = 1; k < kNW; ++k) r = max(r, s[k]);
+  return r;
 }
 
 // (value, index) packed so that a larger u64 is a larger value, then a lower
-// index: the value's order-preserving bits above the complemented index.
+// index: the value's order-preserving bits above the complemented index.  0
+// stands for "no token".
 __device__ __forceinline__ uint32_t f32_order(float v) {
   const uint32_t b = __float_as_uint(v);
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
@@ -215,7 +191,11 @@ __device__ __forceinline__ uint32_t f32_order(float v) {
 __device__ __forceinline__ unsigned long long pack_arg(uint32_t ordered, int idx) {
   return (static_cast<unsigned long long>(ordered) << 32) | uint32_t(~uint32_t(idx));
 }
-__device__ __forceinline__ int arg_index(unsigned long long pk) { return int(~uint32_t(pk)); }
+// The id a row's winner stands for: 0 when no token won.
+__device__ __forceinline__ int64_t winner_id(unsigned long long pk, int vocab) {
+  const int idx = int(~uint32_t(pk));
+  return (pk >> 32) != 0 && idx >= 0 && idx < vocab ? idx : 0;
+}
 
 template <typename F>
 __device__ __forceinline__ F coherent_load(const F* p) {
@@ -226,7 +206,7 @@ __device__ __forceinline__ void coherent_store(F* p, F v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// 16-byte device-coherent (sc1) buffer accesses for the histograms: the
+// 16-byte device-coherent (sc1) buffer store for the histograms: the
 // partials travel between workgroups on different XCDs.
 constexpr int kCacheSc1 = 16;
 constexpr int kBufferWord3 = 0x00020000;
@@ -316,189 +296,294 @@ __device__ __forceinline__ bool has_mass(uint32_t max_key) {
   return max_key != 0u && max_key != kNaN16 && key_to_f32(max_key) != -INFINITY;
 }
 
+// The race value of a token with key kk (> 0) and random bits r; false for a
+// token of mass 0 (-inf), which never wins.  NaN ranks above every number.
+__device__ __forceinline__ bool race_value(uint32_t kk, uint32_t r, float& v, float& s) {
+  if (kk == kNaN16) {
+    v = INFINITY;
+    s = 0.f;
+    return true;
+  }
+  s = key_to_f32(kk);
+  if (s == -INFINITY) return false;
+  v = s * mi::kLog2e - __log2f(-__log2f(u01(r)));
+  return true;
+}
+
+// Lanes 0..n-1 of one wave hold the masses H of n items in key order (the
+// highest last).  In every lane: the item where the mass accumulated from the
+// top reaches `target` -- a < target <= a + H, with a = `above0` + the mass of
+// the items above it; the highest such item if rounding makes several --, or
+// -1; `lowest` = the lowest item with H > 0 (or -1), `a_sel` = a of the
+// item found.
+__device__ __forceinline__ void boundary_search(float H, float above0, float target, int& sel, int& lowest,
+                                                float& a_sel) {
+  const int lane = threadIdx.x & 63;
+  float incl = H;  // mass of the items >= this one
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float y = __shfl_down(incl, o);
+    if (lane + o < 64) incl += y;
+  }
+  float excl = __shfl_down(incl, 1);  // mass of the items above this one
+  if (lane == 63) excl = 0.f;
+  const float a = above0 + excl;
+  const uint64_t hit = __ballot(H > 0.f && a < target && a + H >= target);
+  const uint64_t nonempty = __ballot(H > 0.f);
+  sel = hit ? 63 - __builtin_clzll(hit) : -1;
+  lowest = nonempty ? __builtin_ctzll(nonempty) : -1;
+  a_sel = sel >= 0 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), sel)) : 0.f;
+}
+
 __global__ __launch_bounds__(kT) void sample_pass1(SampleParams p) {
-  __shared__ float bins[kNW][kBins];  // one copy per wave: fewer colliding LDS atomics
-  __shared__ float s_scale[kMaxChunks];
-  __shared__ uint32_t sv[kNW];
-  __shared__ int si[kNW];
-  __shared__ float sf[kNW];
-  __shared__ int s_flag;
-  const int c = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+  __shared__ __align__(16) unsigned long long hist[kBins];
+  __shared__ uint32_t s_max[kNW];
+  const int c = blockIdx.x, row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const RowParams rp = row_params(p, row);
-  const bool hist = !rp.greedy && rp.tp < 1.0f;
-  if (hist)
-    for (int i = tid; i < kNW * kBins; i += kT) (&bins[0][0])[i] = 0.f;
+  const bool top_p = !rp.greedy && rp.tp < 1.0f;
+  const int pc = row * p.chunks + c;
+  static_assert(kBins == 4 * kT, "each thread owns 4 bins");
+  if (pc == 0 && tid == 0) coherent_store(p.off_copy, *p.offset);
+  if (top_p) {
+    const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+    reinterpret_cast<uint4*>(hist)[2 * tid] = z;
+    reinterpret_cast<uint4*>(hist)[2 * tid + 1] = z;
+  }
   uint32_t k[kGroupsPerThread][4];
   int g[kGroupsPerThread];
   chunk_keys(p, row, c, rp, k, g);
-  uint32_t bk = 0;
-  int bi = 0x7fffffff;
-#pragma unroll
-  for (int n = 0; n < kGroupsPerThread; ++n)
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (k[n][e]) better(bk, bi, k[n][e], 4 * g[n] + e);
-  block_argmax<uint32_t>(bk, bi, sv, si, 0u);  // ends with a barrier: bins are zeroed
-  const int pc = row * p.chunks + c;
-  if (rp.greedy) {
-    if (tid == 0) coherent_store(&p.p1_arg[pc], pack_arg(bk, bi));
-  } else {
-    if (tid == 0) coherent_store(&p.p1_max[pc], bk);
-    if (hist && has_mass(bk)) {
-      const float smax_c = key_to_f32(bk) * mi::kLog2e;
+
+  if (!top_p) {
+    // the wave's winner: greedy argmax, or the race over every token
+    unsigned long long win = 0;
+    if (rp.greedy) {
 #pragma unroll
       for (int n = 0; n < kGroupsPerThread; ++n)
 #pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (k[n][e]) win = max(win, pack_arg(k[n][e], 4 * g[n] + e));
+    } else {
+      const uint64_t off = *p.offset;
+#pragma unroll
+      for (int n = 0; n < kGroupsPerThread; ++n) {
+        if (!(k[n][0] | k[n][1] | k[n][2] | k[n][3])) continue;  // past the vocabulary: no Philox block
+        const uint4 r = philox4x32_10(make_uint4(uint32_t(g[n]), uint32_t(row), uint32_t(off), uint32_t(off >> 32)),
+                                      p.seed);
+        const uint32_t rr[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const uint32_t kk = k[n][e];
-          if (kk == 0u || kk == kNaN16) continue;
-          atomicAdd(&bins[tid >> 6][kk >> 6], __builtin_amdgcn_exp2f(key_to_f32(kk) * mi::kLog2e - smax_c));
+          float v, s;
+          if (k[n][e] && race_value(k[n][e], rr[e], v, s)) win = max(win, pack_arg(f32_order(v), 4 * g[n] + e));
         }
-    }
-    if (hist) {
-      __syncthreads();
-      static_assert(kBins == 4 * kT, "one 16-byte store of 4 bins per thread");
-      const __amdgpu_buffer_rsrc_t rb = rsrc_of(p.p1_bins + size_t(pc) * kBins, kBins * sizeof(float));
-      float b4[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        b4[q] = 0.f;
-#pragma unroll
-        for (int c2 = 0; c2 < kNW; ++c2) b4[q] += bins[c2][4 * tid + q];
       }
-      const u32x4_t v = {__float_as_uint(b4[0]), __float_as_uint(b4[1]), __float_as_uint(b4[2]), __float_as_uint(b4[3])};
-      __builtin_amdgcn_raw_buffer_store_b128(v, rb, 16 * tid, 0, kCacheSc1);
     }
-  }
-  if (!last_of_row(&p.cnt1[row], p.chunks, &s_flag)) return;
-
-  // ---- the row's last workgroup
-  const int base = row * p.chunks;
-  if (rp.greedy) {
-    unsigned long long best = 0;
-    for (int cc = tid; cc < p.chunks; cc += kT) best = max(best, coherent_load(&p.p1_arg[base + cc]));
-    uint32_t hi = uint32_t(best >> 32);
-    int lo = arg_index(best);
-    block_argmax<uint32_t>(hi, lo, sv, si, 0u);
-    if (tid == 0) p.out[row] = (hi != 0u && lo < p.vocab) ? lo : 0;
+    win = wave_max_u64(win);
+    if (lane == 0) coherent_store(&p.part[size_t(pc) * kNW + w], win);
     return;
   }
-  uint32_t M = 0;
-  for (int cc = tid; cc < p.chunks; cc += kT) M = max(M, coherent_load(&p.p1_max[base + cc]));
-  {
-    int unused = 0;
-    block_argmax<uint32_t>(M, unused, sv, si, 0u);
+
+  // top-p rows: the chunk max, then the histogram relative to it
+  uint32_t m = 0;
+#pragma unroll
+  for (int n = 0; n < kGroupsPerThread; ++n)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) m = max(m, k[n][e]);
+  const uint32_t cm = block_max(m, s_max);  // its barrier also orders the zeroing
+  if (has_mass(cm)) {
+    // (no NaN key here: it would be the max)
+    const float smax_c = key_to_f32(cm) * mi::kLog2e;
+#pragma unroll
+    for (int n = 0; n < kGroupsPerThread; ++n)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t kk = k[n][e];
+        if (kk == 0u) continue;
+        const unsigned long long q = to_fix(__builtin_amdgcn_exp2f(key_to_f32(kk) * mi::kLog2e - smax_c));
+        if (q) atomicAdd(&hist[kk >> 6], q);
+      }
   }
+  __syncthreads();
+  const uint4 h01 = reinterpret_cast<const uint4*>(hist)[2 * tid];
+  const uint4 h23 = reinterpret_cast<const uint4*>(hist)[2 * tid + 1];
+  const unsigned long long q0 = (static_cast<unsigned long long>(h01.y) << 32) | h01.x;
+  const unsigned long long q1 = (static_cast<unsigned long long>(h01.w) << 32) | h01.z;
+  const unsigned long long q2 = (static_cast<unsigned long long>(h23.y) << 32) | h23.x;
+  const unsigned long long q3 = (static_cast<unsigned long long>(h23.w) << 32) | h23.z;
+  const __amdgpu_buffer_rsrc_t rb = rsrc_of(p.bins + size_t(pc) * kBins, kBins * sizeof(float));
+  const u32x4_t v = {__float_as_uint(from_fix(q0)), __float_as_uint(from_fix(q1)), __float_as_uint(from_fix(q2)),
+                     __float_as_uint(from_fix(q3))};
+  __builtin_amdgcn_raw_buffer_store_b128(v, rb, 16 * tid, 0, kCacheSc1);
+  // super-bin j = bins 32j .. 32j + 31 = threads 8j .. 8j + 7: exact sum over 8 lanes
+  static_assert(kBinsPerSup == 32, "a super-bin is 8 threads' bins");
+  unsigned long long s = q0 + q1 + q2 + q3;
+  s += dpp_u64<mi::kDppQuadSwap1>(s);
+  s += dpp_u64<mi::kDppQuadSwap2>(s);
+  s += dpp_u64<mi::kDppRowHalfMirror>(s);
+  if ((tid & 7) == 0) coherent_store(&p.sup[size_t(pc) * kSup + (tid >> 3)], from_fix(s));
+  if (tid == 0) coherent_store(&p.cmax[pc], cm);
+}
+
+struct RowInfo {
+  float smax;    // row max scaled logit x log2 e
+  int bstar;     // boundary bin, -1: every token is kept
+  float above;   // mass of the bins above it (relative to the row max)
+  float target;  // top_p x total mass (+inf: every key of the boundary bin is kept)
+};
+
+// The top-p boundary of a row from pass 1's chunk partials, in every
+// workgroup of the row.  `mc` = this thread's chunk max (chunk tid), `sv` =
+// the super-bin sums of chunks grp + kGrp * u (super-bin tid % kSup).
+__device__ __forceinline__ RowInfo row_boundary(const SampleParams& p, int row, float tp, uint32_t mc,
+                                                const float (&sv0)[8], float* s_scale, float (*s_part)[kSup],
+                                                uint32_t* s_u32, float* s_f, int* s_i) {
+  const int tid = threadIdx.x, j = tid & (kSup - 1), grp = tid / kSup;
+  const int C = p.chunks, base = row * C;
   RowInfo ri;
-  ri.smax = has_mass(M) ? key_to_f32(M) * mi::kLog2e : 0.f;
   ri.bstar = -1;
   ri.above = 0.f;
   ri.target = 0.f;
-  if (hist && has_mass(M)) {
-    // thread t owns bins 4t .. 4t + 3: H = sum over chunks of the chunk's
-    // bins x 2^(chunk max - row max)
-    // each chunk's scale (0: it carries no mass and wrote no bins), then
-    // its bins, eight chunks' loads in flight at a time
-    for (int cc = tid; cc < p.chunks; cc += kT) {
-      const uint32_t mc = coherent_load(&p.p1_max[base + cc]);
-      s_scale[cc] = has_mass(mc) ? __builtin_amdgcn_exp2f(key_to_f32(mc) * mi::kLog2e - ri.smax) : 0.f;
+  const uint32_t M = block_max(mc, s_u32);
+  ri.smax = has_mass(M) ? key_to_f32(M) * mi::kLog2e : 0.f;
+  if (!has_mass(M)) return ri;  // NaN or no mass: every token is kept
+  if (tid < C) s_scale[tid] = has_mass(mc) ? __builtin_amdgcn_exp2f(key_to_f32(mc) * mi::kLog2e - ri.smax) : 0.f;
+  __syncthreads();
+  // super-bin totals, scaled to the row max, in chunk order
+  float part = 0.f;
+  for (int c0 = 0; c0 < C; c0 += kGrp * 8) {
+    float sv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int cc = c0 + grp + kGrp * u;
+      sv[u] = c0 == 0 ? sv0[u] : (cc < C ? coherent_load(&p.sup[size_t(base + cc) * kSup + j]) : 0.f);
     }
-    __syncthreads();
-    float H[4] = {0.f, 0.f, 0.f, 0.f};
-    const __amdgpu_buffer_rsrc_t rb = rsrc_of(p.p1_bins + size_t(base) * kBins, size_t(p.chunks) * kBins * 4);
-    for (int c0 = 0; c0 < p.chunks; c0 += 8) {
-      u32x4_t v[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        v[u] = __builtin_amdgcn_raw_buffer_load_b128(rb, ((c0 + u) * kBins + 4 * tid) * 4, 0, kCacheSc1);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        if (c0 + u >= p.chunks) break;
-        const float sc = s_scale[c0 + u];
-        if (sc == 0.f) continue;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) H[q] += __uint_as_float(v[u][q]) * sc;
+    for (int u = 0; u < 8; ++u) {
+      const int cc = c0 + grp + kGrp * u;
+      if (cc < C) {
+        const float sc = s_scale[cc];
+        if (sc != 0.f) part += sc * sv[u];
       }
     }
-    const float mine = H[0] + H[1] + H[2] + H[3];
-    const float Z = block_sum(mine, sf);
-    const float target = rp.tp * Z;
-    // mass strictly above bin 4t + 3: the bins of threads t' > t (a suffix
-    // scan over the workgroup: inclusive prefix from the top)
-    float incl = mine;  // becomes sum over threads >= t
-    const int lane = tid & 63, w = tid >> 6;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const float y = __shfl_down(incl, o);
-      if (lane + o < 64) incl += y;
-    }
-    if (lane == 0) sf[w] = incl;  // wave totals
-    __syncthreads();
-    float later = 0.f;
-#pragma unroll
-    for (int q = 0; q < kNW; ++q) later += (q > w) ? sf[q] : 0.f;
-    __syncthreads();
-    float a = incl + later - mine;  // mass of bins above 4t + 3
-    // the boundary: the bin b with H[b] > 0 and above(b) < target <= above(b) + H[b]
-    int pick = -1, lowest = -1;
-    float pick_above = 0.f;
-#pragma unroll
-    for (int q = 3; q >= 0; --q) {
-      if (H[q] > 0.f) {
-        if (pick < 0 && a < target && a + H[q] >= target) {
-          pick = 4 * tid + q;
-          pick_above = a;
-        }
-        lowest = 4 * tid + q;
-      }
-      a += H[q];
-    }
-    // one thread holds the boundary (argmax of "found", lowest bin first);
-    // if rounding left none, the lowest non-empty bin (every token kept down
-    // to it)
-    uint32_t has = pick >= 0 ? 1u : 0u;
-    int bsel = pick >= 0 ? pick : 0x7fffffff;
-    block_argmax<uint32_t>(has, bsel, sv, si, 0u);
-    uint32_t nonempty = lowest >= 0 ? 1u : 0u;
-    int lo_bin = lowest >= 0 ? lowest : 0x7fffffff;
-    block_argmax<uint32_t>(nonempty, lo_bin, sv, si, 0u);
-    if (has) {
-      ri.bstar = bsel;
-      // the thread that found it publishes its `above`
-      if (pick >= 0) sf[0] = pick_above;
-      __syncthreads();
-      ri.above = sf[0];
-    } else {
-      ri.bstar = lo_bin;
-      ri.above = 0.f;  // unused: the boundary key search falls back to the lowest non-empty key
-    }
-    ri.target = has ? target : INFINITY;
   }
-  if (tid == 0) p.info[row] = ri;
+  s_part[grp][j] = part;
+  __syncthreads();
+  if (tid < 64) {
+    float S = 0.f;
+    if (tid < kSup)
+#pragma unroll
+      for (int q = 0; q < kGrp; ++q) S += s_part[q][tid];
+    float Z = S;
+    Z += __shfl_xor(Z, 1);
+    Z += __shfl_xor(Z, 2);
+    Z += __shfl_xor(Z, 4);
+    Z += __shfl_xor(Z, 8);
+    Z += __shfl_xor(Z, 16);
+    Z += __shfl_xor(Z, 32);
+    const float target = tp * Z;
+    int sel, lowest;
+    float a_sel;
+    boundary_search(S, 0.f, target, sel, lowest, a_sel);
+    if (tid == 0) {
+      // rounding left no super-bin: keep every token down to the lowest
+      // non-empty one
+      s_i[0] = sel >= 0 ? sel : max(lowest, 0);  // (the row max's super-bin is never empty)
+      s_f[0] = a_sel;
+      s_f[1] = sel >= 0 ? target : INFINITY;
+    }
+  }
+  __syncthreads();
+  const int sstar = s_i[0];
+  const float aboveS = s_f[0], target = s_f[1];
+  // the bins of the boundary super-bin, scaled to the row max, in chunk order
+  part = 0.f;
+  for (int c0 = 0; c0 < C; c0 += kGrp * 8) {
+    float bv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int cc = c0 + grp + kGrp * u;
+      bv[u] = cc < C ? coherent_load(&p.bins[size_t(base + cc) * kBins + sstar * kBinsPerSup + j]) : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int cc = c0 + grp + kGrp * u;
+      if (cc < C) {
+        const float sc = s_scale[cc];
+        if (sc != 0.f) part += sc * bv[u];
+      }
+    }
+  }
+  s_part[grp][j] = part;
+  __syncthreads();
+  if (tid < 64) {
+    float B = 0.f;
+    if (tid < kSup)
+#pragma unroll
+      for (int q = 0; q < kGrp; ++q) B += s_part[q][tid];
+    int sel, lowest;
+    float a_sel;
+    boundary_search(B, aboveS, target, sel, lowest, a_sel);
+    if (tid == 0) {
+      // none found (rounding, or every token kept down to this super-bin):
+      // the lowest non-empty bin, all of its keys kept
+      s_i[1] = sstar * kBinsPerSup + (sel >= 0 ? sel : (lowest >= 0 ? lowest : 0));
+      s_f[2] = sel >= 0 ? a_sel : 0.f;
+      s_f[3] = sel >= 0 ? target : INFINITY;
+    }
+  }
+  __syncthreads();
+  ri.bstar = s_i[1];
+  ri.above = s_f[2];
+  ri.target = s_f[3];
+  return ri;
 }
 
 __global__ __launch_bounds__(kT) void sample_pass2(SampleParams p) {
-  __shared__ float sub_mass[kNW][kSub];  // one copy per wave
-  __shared__ unsigned long long sub_best[kNW][kSub];
-  __shared__ float svf[kNW];
-  __shared__ int si[kNW];
+  __shared__ float s_scale[kMaxChunks];
+  __shared__ float s_part[kGrp][kSup];
+  __shared__ unsigned long long sub_mass[kSub];
+  __shared__ unsigned long long sub_best[kSub];
+  __shared__ unsigned long long s_m64[kNW][kSub];
+  __shared__ unsigned long long s_b64[kNW][kSub];
+  __shared__ unsigned long long s_win[kNW];
+  __shared__ unsigned long long s_win2[kNW];
+  __shared__ uint32_t s_u32[kNW];
+  __shared__ float s_f[4];
+  __shared__ int s_i[2];
   __shared__ int s_flag;
-  const int c = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+  const int c = blockIdx.x, row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const RowParams rp = row_params(p, row);
-  if (!rp.greedy) {
-    const RowInfo ri = p.info[row];
-    const uint64_t off = *p.offset;
-    if (ri.bstar >= 0) {
-      (&sub_mass[0][0])[tid] = 0.f;  // kT == kNW * kSub
-      (&sub_best[0][0])[tid] = 0ull;
+  const bool top_p = !rp.greedy && rp.tp < 1.0f;
+  const int C = p.chunks, base = row * C;
+  if (!top_p) {
+    // rows drawn in pass 1: the best of the row's wave winners
+    if (c == 0) {
+      unsigned long long best = 0;
+      for (int i = tid; i < C * kNW; i += kT) best = max(best, coherent_load(&p.part[size_t(base) * kNW + i]));
+      best = block_max(best, s_win);
+      if (tid == 0) p.out[row] = winner_id(best, p.vocab);
     }
-    __syncthreads();
+  } else {
+    if (tid < kSub) {
+      sub_mass[tid] = 0ull;
+      sub_best[tid] = 0ull;
+    }
+    // pass 1's partials of the row (chunk maxima, the first 64 chunks'
+    // super-bin sums), then this chunk's logits, all in flight together
+    const uint32_t mc = tid < C ? coherent_load(&p.cmax[base + tid]) : 0u;
+    float sv0[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int cc = tid / kSup + kGrp * u;
+      sv0[u] = cc < C ? coherent_load(&p.sup[size_t(base + cc) * kSup + (tid & (kSup - 1))]) : 0.f;
+    }
+    const uint64_t off = coherent_load(p.off_copy);
     uint32_t k[kGroupsPerThread][4];
     int g[kGroupsPerThread];
     chunk_keys(p, row, c, rp, k, g);
+    const RowInfo ri = row_boundary(p, row, rp.tp, mc, sv0, s_scale, s_part, s_u32, s_f, s_i);
+
     const uint32_t kmin = ri.bstar < 0 ? 1u : uint32_t(ri.bstar) << 6;  // lowest key that may be kept
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    unsigned long long win = 0;
 #pragma unroll
     for (int n = 0; n < kGroupsPerThread; ++n) {
       bool any = false;
@@ -511,113 +596,82 @@ __global__ __launch_bounds__(kT) void sample_pass2(SampleParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t kk = k[n][e];
-        if (kk < kmin) continue;
-        const int i = 4 * g[n] + e;
-        float v;
-        float sc = 0.f;
-        if (kk == kNaN16) {
-          v = INFINITY;
-        } else {
-          sc = key_to_f32(kk);
-          if (sc == -INFINITY) continue;
-          v = sc * mi::kLog2e - __log2f(-__log2f(u01(rr[e])));
-        }
+        float v, s;
+        if (kk < kmin || !race_value(kk, rr[e], v, s)) continue;
+        const unsigned long long pk = pack_arg(f32_order(v), 4 * g[n] + e);
         if (ri.bstar >= 0 && int(kk >> 6) == ri.bstar) {
-          atomicAdd(&sub_mass[tid >> 6][kk & 63], __builtin_amdgcn_exp2f(sc * mi::kLog2e - ri.smax));
-          atomicMax(&sub_best[tid >> 6][kk & 63], pack_arg(f32_order(v), i));
+          // (no NaN key here: the row max would be NaN)
+          const unsigned long long q = to_fix(__builtin_amdgcn_exp2f(s * mi::kLog2e - ri.smax));
+          if (q) atomicAdd(&sub_mass[kk & 63], q);
+          atomicMax(&sub_best[kk & 63], pk);
         } else {
-          betterf(bv, bi, v, i);
+          win = max(win, pk);
         }
       }
     }
-    block_argmax<float>(bv, bi, svf, si, -INFINITY);  // ends with a barrier: sub_* are complete
-    const int pc = row * p.chunks + c;
-    if (tid == 0) coherent_store(&p.p2_best[pc], bi == 0x7fffffff ? 0ull : pack_arg(f32_order(bv), bi));
+    win = block_max(win, s_win);  // its barrier also completes sub_*
+    const int pc = base + c;
+    if (tid == 0) coherent_store(&p.best[pc], win);
     if (ri.bstar >= 0 && tid < kSub) {
-      float m = 0.f;
-      unsigned long long b = 0;
-#pragma unroll
-      for (int c2 = 0; c2 < kNW; ++c2) {
-        m += sub_mass[c2][tid];
-        b = max(b, sub_best[c2][tid]);
-      }
-      coherent_store(&p.p2_sub_mass[size_t(pc) * kSub + tid], m);
-      coherent_store(&p.p2_sub_best[size_t(pc) * kSub + tid], b);
+      coherent_store(&p.sub_mass[size_t(pc) * kSub + tid], sub_mass[tid]);
+      coherent_store(&p.sub_best[size_t(pc) * kSub + tid], sub_best[tid]);
     }
-    if (last_of_row(&p.cnt2[row], p.chunks, &s_flag)) {
-      const int base = row * p.chunks;
-      unsigned long long best = 0;
-      for (int cc = tid; cc < p.chunks; cc += kT) best = max(best, coherent_load(&p.p2_best[base + cc]));
+    if (last_of_row(&p.cnt[row], C, &s_flag)) {
+      unsigned long long bb = 0;
+      for (int cc = tid; cc < C; cc += kT) bb = max(bb, coherent_load(&p.best[base + cc]));
       if (ri.bstar >= 0) {
-        // wave 0: lane s holds key (bstar << 6) | s of the boundary bin
-        if (tid < 64) {
-          float m = 0.f;
-          unsigned long long b = 0;
-          for (int c0 = 0; c0 < p.chunks; c0 += 8) {
-            float mv[8];
-            unsigned long long bv8[8];
+        // key `lane` of the boundary bin over chunks w, w + kNW, ... (8 in flight)
+        unsigned long long m = 0, b = 0;
+        for (int c0 = w; c0 < C; c0 += kNW * 8) {
+          unsigned long long mv[8], bv[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-              const int cc = min(c0 + u, p.chunks - 1);
-              mv[u] = coherent_load(&p.p2_sub_mass[size_t(base + cc) * kSub + tid]);
-              bv8[u] = coherent_load(&p.p2_sub_best[size_t(base + cc) * kSub + tid]);
-            }
+          for (int u = 0; u < 8; ++u) {
+            const int cc = min(c0 + kNW * u, C - 1);
+            mv[u] = coherent_load(&p.sub_mass[size_t(base + cc) * kSub + lane]);
+            bv[u] = coherent_load(&p.sub_best[size_t(base + cc) * kSub + lane]);
+          }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-              if (c0 + u >= p.chunks) break;
-              m += mv[u];
-              b = max(b, bv8[u]);
-            }
+          for (int u = 0; u < 8; ++u) {
+            if (c0 + kNW * u >= C) break;
+            m += mv[u];
+            b = max(b, bv[u]);
           }
-          // mass of the bin's keys above lane s: suffix sum over lanes > s
-          float incl = m;
-#pragma unroll
-          for (int o = 1; o < 64; o <<= 1) {
-            const float y = __shfl_down(incl, o);
-            if (tid + o < 64) incl += y;
-          }
-          const float above = ri.above + incl - m;
-          const uint64_t hit = __ballot(m > 0.f && above < ri.target && above + m >= ri.target);
-          const uint64_t nonempty = __ballot(m > 0.f);
-          // the boundary key; if rounding left none, the lowest non-empty key
-          const int sstar = hit ? 63 - __builtin_clzll(hit) : (nonempty ? __builtin_ctzll(nonempty) : 64);
-          if (tid < sstar) b = 0;  // below the boundary: not kept
-          // max over the wave
-          for (int o = 32; o > 0; o >>= 1) {
-            const unsigned long long ob =
-                (static_cast<unsigned long long>(uint32_t(__shfl_xor(int(b >> 32), o))) << 32) |
-                uint32_t(__shfl_xor(int(uint32_t(b)), o));
-            b = max(b, ob);
-          }
-          if (tid == 0) sub_best[0][0] = b;
         }
-        __syncthreads();
-        best = max(best, sub_best[0][0]);
+        s_m64[w][lane] = m;
+        s_b64[w][lane] = b;
       }
-      // the row's best over its chunks (thread 0 holds chunk 0's; reduce)
-      {
-        uint32_t hi = uint32_t(best >> 32);
-        int lo = best ? arg_index(best) : 0x7fffffff;
-        block_argmax<uint32_t>(hi, lo, reinterpret_cast<uint32_t*>(svf), si, 0u);
-        if (tid == 0) p.out[row] = (hi != 0u && lo < p.vocab) ? lo : 0;
+      bb = wave_max_u64(bb);
+      if (lane == 0) s_win2[w] = bb;
+      __syncthreads();
+      if (tid < 64) {
+        unsigned long long best = max(max(s_win2[0], s_win2[1]), max(s_win2[2], s_win2[3]));
+        if (ri.bstar >= 0) {
+          unsigned long long m = 0, b = 0;
+#pragma unroll
+          for (int q = 0; q < kNW; ++q) {
+            m += s_m64[q][lane];
+            b = max(b, s_b64[q][lane]);
+          }
+          // the boundary key; if rounding left none, the lowest non-empty key
+          int sel, lowest;
+          float a_sel;
+          boundary_search(from_fix(m), ri.above, ri.target, sel, lowest, a_sel);
+          const int sstar = sel >= 0 ? sel : (lowest >= 0 ? lowest : 64);
+          if (lane < sstar) b = 0;  // below the boundary: not kept
+          best = max(best, wave_max_u64(b));
+        }
+        if (tid == 0) p.out[row] = winner_id(best, p.vocab);
       }
     }
   }
-  // every workgroup of the grid counts itself; the last one advances the
-  // draw offset (every workgroup has read it by then)
-  if (tid == 0) {
-    const int total = p.chunks * p.batch;
-    if (__hip_atomic_fetch_add(p.done, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == total - 1) {
-      coherent_store(p.offset, coherent_load(p.offset) + 1);
-      coherent_store(p.done, 0);
-    }
-  }
+  // the next call's offset: every reader of the offset ran in pass 1
+  if (c == 0 && row == 0 && tid == 0) coherent_store(p.offset, coherent_load(p.off_copy) + 1);
 }
 
 constexpr int kMaxRows = 65535;
 
 struct SampleLayout {
-  size_t cnt1, cnt2, done, info, p1_max, p1_arg, p1_bins, p2_best, p2_sub_mass, p2_sub_best, total;
+  size_t cnt, off_copy, part, cmax, sup, bins, best, sub_mass, sub_best, total;
 };
 
 SampleLayout sample_layout(int batch, int vocab) {
@@ -633,16 +687,15 @@ SampleLayout sample_layout(int batch, int vocab) {
   // counters at fixed offsets, sized for the largest batch a call takes, so
   // calls of different batch sizes on one workspace never lay partials over
   // them (every call leaves them at zero)
-  L.cnt1 = take(size_t(kMaxRows) * sizeof(int));
-  L.cnt2 = take(size_t(kMaxRows) * sizeof(int));
-  L.done = take(sizeof(int));
-  L.info = take(size_t(batch) * sizeof(RowInfo));
-  L.p1_max = take(rc * sizeof(uint32_t));
-  L.p1_arg = take(rc * sizeof(unsigned long long));
-  L.p1_bins = take(rc * kBins * sizeof(float));
-  L.p2_best = take(rc * sizeof(unsigned long long));
-  L.p2_sub_mass = take(rc * kSub * sizeof(float));
-  L.p2_sub_best = take(rc * kSub * sizeof(unsigned long long));
+  L.cnt = take(size_t(kMaxRows) * sizeof(int));
+  L.off_copy = take(sizeof(uint64_t));
+  L.part = take(rc * kNW * sizeof(unsigned long long));
+  L.cmax = take(rc * sizeof(uint32_t));
+  L.sup = take(rc * kSup * sizeof(float));
+  L.bins = take(rc * kBins * sizeof(float));
+  L.best = take(rc * sizeof(unsigned long long));
+  L.sub_mass = take(rc * kSub * sizeof(unsigned long long));
+  L.sub_best = take(rc * kSub * sizeof(unsigned long long));
   L.total = off;
   return L;
 }
@@ -686,16 +739,15 @@ extern "C" int mi_sample(const void* logits, int64_t logits_row_stride, int32_t 
   sp.seed = make_uint2(uint32_t(seed), uint32_t(seed >> 32));
   sp.offset = rng_offset;
   sp.out = out_tokens;
-  sp.cnt1 = reinterpret_cast<int*>(ws + L.cnt1);
-  sp.cnt2 = reinterpret_cast<int*>(ws + L.cnt2);
-  sp.done = reinterpret_cast<int*>(ws + L.done);
-  sp.info = reinterpret_cast<RowInfo*>(ws + L.info);
-  sp.p1_max = reinterpret_cast<uint32_t*>(ws + L.p1_max);
-  sp.p1_arg = reinterpret_cast<unsigned long long*>(ws + L.p1_arg);
-  sp.p1_bins = reinterpret_cast<float*>(ws + L.p1_bins);
-  sp.p2_best = reinterpret_cast<unsigned long long*>(ws + L.p2_best);
-  sp.p2_sub_mass = reinterpret_cast<float*>(ws + L.p2_sub_mass);
-  sp.p2_sub_best = reinterpret_cast<unsigned long long*>(ws + L.p2_sub_best);
+  sp.cnt = reinterpret_cast<int*>(ws + L.cnt);
+  sp.off_copy = reinterpret_cast<uint64_t*>(ws + L.off_copy);
+  sp.part = reinterpret_cast<unsigned long long*>(ws + L.part);
+  sp.cmax = reinterpret_cast<uint32_t*>(ws + L.cmax);
+  sp.sup = reinterpret_cast<float*>(ws + L.sup);
+  sp.bins = reinterpret_cast<float*>(ws + L.bins);
+  sp.best = reinterpret_cast<unsigned long long*>(ws + L.best);
+  sp.sub_mass = reinterpret_cast<unsigned long long*>(ws + L.sub_mass);
+  sp.sub_best = reinterpret_cast<unsigned long long*>(ws + L.sub_best);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid{unsigned(chunks), unsigned(batch_size), 1u};
   hipLaunchKernelGGL(sample_pass1, grid, dim3(kT), 0, s, sp);
