@@ -59,14 +59,18 @@ constexpr float kLazyRescale = 8.0f;
 #ifndef PREFILL_RS_PAD
 #define PREFILL_RS_PAD 32
 #endif
-// Row blocks of 16 per wave for head_dim 64 / 128 (256: always 1).
+// K / V tiles staged straight to LDS by the gfx950 buffer loads with the
+// `lds` modifier (no staging registers, no LDS store instructions).  A wave's
+// load instruction fills 1 KB of LDS, lane l at byte 16 l, so the rows are
+// unpadded and a 16-byte chunk's place in its row is permuted instead
+// (chunk_slot) to keep the reads off shared banks.
+#ifndef PREFILL_DMA
+#define PREFILL_DMA 1
+#endif
 // Output staging: pad bytes after every 8 columns (32 bytes each) of a
 // column-major 16-row block, so the 8-byte writes of a half wave and the
 // transpose reads of two lane groups fall on distinct banks.
 constexpr int kOutPad = 144;
-#ifndef PREFILL_MAXRB
-#define PREFILL_MAXRB 2
-#endif
 
 struct alignas(32) PrefillTile {
   int b;
@@ -89,10 +93,23 @@ struct PrefillHeader {
 // Waves per workgroup.
 constexpr int waves_for(int /*head_dim*/) { return 4; }
 
-// Query positions per workgroup: about `rows` (position, head) rows, where
-// rows = 128 for head_dim <= 128 (two row blocks per wave) and 64 for 256.
+// Row blocks of 16 (position, head) rows per wave: head_dim 256 one; head_dim
+// 128 three when 192 rows make 12 whole row blocks (group 1, 2, 3, 4, 6:
+// each K / V operand read from LDS then feeds three blocks -- Mistral-7B
+// heads, 32 prompts U[128, 1024]: 183 -> 170 us), else two (with group 5, 7
+// or 8 a third block would often be empty and its MFMAs wasted: group 8
+// 319 -> 378 us); head_dim 64 two.
+int row_blocks(int group, int head_dim) {
+  if (head_dim > 128) return 1;
+  if (head_dim == 128 && (192 / group) / 16 * 16 * group == 192) return 3;
+  return 2;
+}
+
+// Query positions per workgroup: bm = (16 * waves * row blocks per wave) /
+// group rounded down to a multiple of 16 (at least 16); 64 / group for
+// head_dim 256.
 int rows_per_tile(int group, int head_dim) {
-  const int rows = head_dim <= 128 ? 16 * waves_for(head_dim) * PREFILL_MAXRB : 64;
+  const int rows = head_dim <= 128 ? 16 * waves_for(head_dim) * row_blocks(group, head_dim) : 64;
   const int bm = (rows / group) / 16 * 16;
   return bm < kMinRows ? kMinRows : bm;
 }
@@ -215,6 +232,14 @@ __device__ __forceinline__ s16x4_t lds_read_tr16(const lds_t* p) {
   typedef __attribute__((address_space(3))) bf16x4_t lds_v4;
   return __builtin_bit_cast(s16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4*)p));
 }
+// 16 bytes per lane from a buffer straight to LDS: lane l's bytes land at
+// dst + 16 l (dst wave-uniform).  The builtin exists for the device pass only
+// (the host pass would drop the kernel stubs that reference it).
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, lds_t* dst, int voffset, int soffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)dst, 16, voffset, soffset, 0, 0);
+#endif
+}
 __device__ __forceinline__ float max_xor16(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -236,6 +261,16 @@ __device__ __forceinline__ float sum_xor32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Slot (16-byte unit of the row) where chunk c of tile row r is staged when
+// the rows are unpadded: c XOR a per-row value, chosen so the 8 rows of a K
+// read group (ds_read_b128: 8 lanes at a time, one row each, same chunk) and
+// the 4 rows x 32 bytes of a V transpose-read group land on distinct banks.
+template <int D>
+__device__ __forceinline__ int chunk_slot(int r, int c) {
+  if constexpr (D == 64) return c ^ (((r >> 1) & 3) << 1);  // 128-byte rows: two per bank period
+  else return c ^ (((r & 7) << 1) | ((r >> 3) & 1));         // 256 / 512-byte rows
+}
+
 template <int D, int MAXRB_>
 struct PrefillTraits {
   static constexpr int WAVES = waves_for(D);
@@ -245,15 +280,19 @@ struct PrefillTraits {
   static constexpr int CPR = D / 8;                // 16-byte chunks per token row
   static constexpr int LOADS = kKvTile * CPR / THREADS;  // 16-byte loads per thread per tile, K and V each
   static_assert(LOADS >= 1 && kKvTile * CPR % THREADS == 0, "tile staging split");
-  static constexpr int RS = D * 2 + PREFILL_RS_PAD;  // LDS row stride (the pad spreads the banks)
+  static constexpr int RS = PREFILL_DMA ? D * 2 : D * 2 + PREFILL_RS_PAD;  // LDS row stride
   static constexpr int TILE = kKvTile * RS;        // bytes of one staged K or V tile
   static constexpr int MAXRB = MAXRB_;             // row blocks per wave
+  static constexpr int OUT_BLK = 8 * 32 + kOutPad;  // output staging: bytes per 8 columns
+  static constexpr int OB = D / 8 * OUT_BLK;         // output staging: bytes per row block
+  // LDS: the double-buffered K / V tiles, reused for the output staging
+  static constexpr int SMEM = 2 * 2 * TILE > WAVES * MAXRB * OB ? 2 * 2 * TILE : WAVES * MAXRB * OB;
 };
 
 template <int D, int MAXRB>
 __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_eu(D <= 128 ? PREFILL_WAVES : 1))) void prefill_run_kernel(RunParams p) {
   using T = PrefillTraits<D, MAXRB>;
-  __shared__ __attribute__((aligned(16))) char smem[2 * 2 * T::TILE];  // [buffer][K, V]
+  __shared__ __attribute__((aligned(16))) char smem[T::SMEM];  // [buffer][K, V], then the output rows
   lds_t* lds = (lds_t*)smem;
 
   const int tile_idx = int(blockIdx.x) / p.hkv;
@@ -323,14 +362,29 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
   // the size stops after its valid V rows, so the V rows past kv_len read as
   // zeros: P is 0 there, but 0 * NaN would poison the MFMA).  No address
   // arithmetic or branches per load.
-  constexpr int TPL = T::THREADS / T::CPR;
-  const int ltok = int(threadIdx.x) / T::CPR, ldc = int(threadIdx.x) - ltok * T::CPR;
   const int tok_bytes = p.hkv * D * 2;
   const int kv_bytes = kPageSize * tok_bytes;
   const int page_bytes = 2 * kv_bytes;
   const int npages_req = (t.kv_len + kPageSize - 1) / kPageSize;
   const int last_rows = t.kv_len - (npages_req - 1) * kPageSize;
   int voff[T::LOADS], pit[T::LOADS];
+#if PREFILL_DMA
+  // Load i of wave w fills 1 KB block b = WAVES i + w of the tile: RPB rows,
+  // lane l taking row b RPB + l / CPR and slot l % CPR of it, i.e. the chunk
+  // chunk_slot(row, slot) (the permutation is its own inverse); a block lies
+  // inside one page, so the page index is wave-uniform.
+  constexpr int RPB = 1024 / (D * 2);
+  const int wv = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+#pragma unroll
+  for (int i = 0; i < T::LOADS; ++i) {
+    const int bk = T::WAVES * i + wv;
+    const int tr = bk * RPB + lane / T::CPR;
+    pit[i] = __builtin_amdgcn_readfirstlane(bk * RPB / kPageSize);
+    voff[i] = (tr % kPageSize) * tok_bytes + hkv * D * 2 + chunk_slot<D>(tr, lane % T::CPR) * 16;
+  }
+#else
+  constexpr int TPL = T::THREADS / T::CPR;
+  const int ltok = int(threadIdx.x) / T::CPR, ldc = int(threadIdx.x) - ltok * T::CPR;
 #pragma unroll
   for (int i = 0; i < T::LOADS; ++i) {
     const int tt = ltok + TPL * i;
@@ -338,6 +392,7 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
     voff[i] = (tt % kPageSize) * tok_bytes + hkv * D * 2 + ldc * 16;
   }
   u32x4_t kreg[T::LOADS], vreg[T::LOADS];
+#endif
   int pid[T::LOADS];
   // page ids through the constant address space: a uniform index then
   // compiles to a scalar load (kv_indices is not written during the launch)
@@ -353,7 +408,7 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
       pid[i] = (kt < ntile && pg_idx < npages_req) ? v : -1;
     }
   };
-  auto load_tile = [&](int kt) {
+  auto load_tile = [&](int kt, int buf) {
 #pragma unroll
     for (int i = 0; i < T::LOADS; ++i) {
       const int pg = pid[i];
@@ -362,11 +417,19 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
       const int size = !ok ? 0 : (pg_idx == npages_req - 1 ? kv_bytes + last_rows * tok_bytes : page_bytes);
       const char* base = reinterpret_cast<const char*>(p.pool) + (ok ? int64_t(pg) * page_bytes : 0);
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, size, kBufferWord3);
+#if PREFILL_DMA
+      lds_t* kdst = lds + buf * 2 * T::TILE + 1024 * (T::WAVES * i + wv);
+      lds_dma16(rs, kdst, voff[i], 0);
+      lds_dma16(rs, kdst + T::TILE, voff[i], kv_bytes);
+#else
+      (void)buf;
       kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[i], 0, 0);
       vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[i], kv_bytes, 0);
+#endif
     }
   };
   auto store_tile = [&](int buf) {
+#if !PREFILL_DMA
     lds_t* kl = lds + buf * 2 * T::TILE + ltok * T::RS + ldc * 16;
     lds_t* vl = kl + T::TILE;
 #pragma unroll
@@ -374,11 +437,14 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
       lds_store16(kl + TPL * i * T::RS, kreg[i]);
       lds_store16(vl + TPL * i * T::RS, vreg[i]);
     }
+#else
+    (void)buf;
+#endif
   };
 
   if (ntile > 0) {
     fetch_ids(0);
-    load_tile(0);
+    load_tile(0, 0);
     fetch_ids(1);
     store_tile(0);
   }
@@ -389,10 +455,25 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
 
+  // LDS read offsets inside a staged tile: K row kb 16 + n (chunk 4 s + g) for
+  // the score operand, V rows 4 g + n / 4 (bytes 32 j + 8 (n & 3)) for the
+  // transpose reads; tile rows are r and r + 16 k, whose permutation depends
+  // on r % 16 only.
+  int koff[T::KSTEPS], voff_lds[T::NT];
+#pragma unroll
+  for (int s2 = 0; s2 < T::KSTEPS; ++s2)
+    koff[s2] = PREFILL_DMA ? n * T::RS + chunk_slot<D>(n, 4 * s2 + g) * 16 : n * T::RS + (4 * s2 + g) * 16;
+#pragma unroll
+  for (int j = 0; j < T::NT; ++j) {
+    const int vr = 4 * g + (n >> 2);
+    voff_lds[j] = PREFILL_DMA ? vr * T::RS + chunk_slot<D>(vr, 2 * j + ((n & 3) >> 1)) * 16 + (n & 1) * 8
+                              : vr * T::RS + (n & 3) * 8 + 32 * j;
+  }
+
   for (int kt = 0; kt < ntile; ++kt) {
     const int buf = kt & 1;
     if (kt + 1 < ntile) {
-      load_tile(kt + 1);
+      load_tile(kt + 1, buf ^ 1);
       fetch_ids(kt + 2);
     }
     const int kv0 = kt * kKvTile;
@@ -422,7 +503,7 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
           mi::bf16x8_t ka[T::KSTEPS];
 #pragma unroll
           for (int s = 0; s < T::KSTEPS; ++s)
-            ka[s] = __builtin_bit_cast(mi::bf16x8_t, lds_load16(kl + (kb * 16 + n) * T::RS + (4 * s + g) * 16));
+            ka[s] = __builtin_bit_cast(mi::bf16x8_t, lds_load16(kl + kb * 16 * T::RS + koff[s]));
 #pragma unroll
           for (int r = 0; r < T::MAXRB; ++r) {
             mi::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
@@ -500,20 +581,61 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
                                                       bf16x8_v));
           }
           // ---- O += P V over key blocks (2h, 2h + 1)
-          const lds_t* v0 = vl + (2 * h * 16 + 4 * g + (n >> 2)) * T::RS + (n & 3) * 8;
+          const lds_t* v0 = vl + 2 * h * 16 * T::RS;
+#if PREFILL_DMA
+          // The transpose reads go through inline asm here: with the builtin the
+          // compiler waited for every load to LDS in flight (the next tile's)
+          // before the first of them.  One statement per group of 4 columns:
+          // 8 reads (the second page's rows 16 * RS further) and the wait for
+          // them, so its outputs hold the data when it ends.
+          static_assert(T::NT % 4 == 0, "column groups of 4");
+          const uint32_t vb0 = uint32_t(reinterpret_cast<uintptr_t>(v0));
+#pragma unroll
+          for (int q = 0; q < T::NT / 4; ++q) {
+            const int j0 = 4 * q;
+            u32x2_t ra[4], rb[4];
+            asm volatile(
+                "ds_read_b64_tr_b16 %0, %8\n\t"
+                "ds_read_b64_tr_b16 %1, %8 offset:%12\n\t"
+                "ds_read_b64_tr_b16 %2, %9\n\t"
+                "ds_read_b64_tr_b16 %3, %9 offset:%12\n\t"
+                "ds_read_b64_tr_b16 %4, %10\n\t"
+                "ds_read_b64_tr_b16 %5, %10 offset:%12\n\t"
+                "ds_read_b64_tr_b16 %6, %11\n\t"
+                "ds_read_b64_tr_b16 %7, %11 offset:%12\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(ra[0]), "=&v"(rb[0]), "=&v"(ra[1]), "=&v"(rb[1]), "=&v"(ra[2]), "=&v"(rb[2]), "=&v"(ra[3]),
+                  "=&v"(rb[3])
+                : "v"(vb0 + voff_lds[j0]), "v"(vb0 + voff_lds[j0 + 1]), "v"(vb0 + voff_lds[j0 + 2]),
+                  "v"(vb0 + voff_lds[j0 + 3]), "i"(16 * T::RS)
+                : "memory");
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+              const mi::bf16x8_t vb =
+                  __builtin_bit_cast(mi::bf16x8_t, u32x4_t{ra[jj].x, ra[jj].y, rb[jj].x, rb[jj].y});
+#pragma unroll
+              for (int r = 0; r < T::MAXRB; ++r) o[r][j0 + jj] = mi::mfma_16x16x32_bf16(pa[r], vb, o[r][j0 + jj]);
+            }
+          }
+#else
           const lds_t* v1 = v0 + 16 * T::RS;
 #pragma unroll
           for (int j = 0; j < T::NT; ++j) {
-            const s16x4_t a = lds_read_tr16(v0 + 32 * j), b = lds_read_tr16(v1 + 32 * j);
+            const s16x4_t a = lds_read_tr16(v0 + voff_lds[j]), b = lds_read_tr16(v1 + voff_lds[j]);
             const mi::bf16x8_t vb =
                 __builtin_bit_cast(mi::bf16x8_t, (s16x8_t){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]});
 #pragma unroll
             for (int r = 0; r < T::MAXRB; ++r) o[r][j] = mi::mfma_16x16x32_bf16(pa[r], vb, o[r][j]);
           }
+#endif
         }
       }
     }
     if (kt + 1 < ntile) store_tile(buf ^ 1);
+#if PREFILL_DMA
+    // the next tile's rows are in LDS (the loads went straight there)
+    if (kt + 1 < ntile) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+#endif
     __syncthreads();
   }
 
@@ -526,9 +648,8 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
   // n: two reads give 16 contiguous bytes of an output row, one 16-byte store
   // through a descriptor over the tile's output rows (rows past the tile get
   // an out-of-range offset, so the stores are unconditional).
-  constexpr int kOutBlk = 8 * 32 + kOutPad;  // bytes per 8 columns
-  constexpr int OB = D / 8 * kOutBlk;        // bytes per row block
-  static_assert(T::WAVES * T::MAXRB * OB <= 2 * 2 * T::TILE, "output staging fits the K / V buffers");
+  constexpr int kOutBlk = T::OUT_BLK;
+  constexpr int OB = T::OB;
   lds_t* const ob = lds + w * T::MAXRB * OB;
   const int wcol = n * 32 + (n >> 3) * kOutPad + 8 * g;
 #pragma unroll
@@ -654,8 +775,13 @@ extern "C" int mi_prefill_run(void* workspace, size_t workspace_bytes, const voi
   const dim3 g{static_cast<uint32_t>(grid), 1u, 1u};
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (head_dim) {
-    case 64: hipLaunchKernelGGL((prefill_run_kernel<64, PREFILL_MAXRB>), g, dim3(64 * waves_for(64)), 0, s, rp); break;
-    case 128: hipLaunchKernelGGL((prefill_run_kernel<128, PREFILL_MAXRB>), g, dim3(64 * waves_for(128)), 0, s, rp); break;
+    case 64: hipLaunchKernelGGL((prefill_run_kernel<64, 2>), g, dim3(64 * waves_for(64)), 0, s, rp); break;
+    case 128:
+      if (row_blocks(rp.group, 128) == 3)
+        hipLaunchKernelGGL((prefill_run_kernel<128, 3>), g, dim3(64 * waves_for(128)), 0, s, rp);
+      else
+        hipLaunchKernelGGL((prefill_run_kernel<128, 2>), g, dim3(64 * waves_for(128)), 0, s, rp);
+      break;
     default: hipLaunchKernelGGL((prefill_run_kernel<256, 1>), g, dim3(64 * waves_for(256)), 0, s, rp); break;
   }
   return mi::check_launch("prefill_run_kernel");
