@@ -262,13 +262,17 @@ __device__ __forceinline__ float sum_xor32(float x) {
 }
 
 // Slot (16-byte unit of the row) where chunk c of tile row r is staged when
-// the rows are unpadded: c XOR a per-row value, chosen so the 8 rows of a K
-// read group (ds_read_b128: 8 lanes at a time, one row each, same chunk) and
-// the 4 rows x 32 bytes of a V transpose-read group land on distinct banks.
+// the rows are unpadded: c XOR a per-row value.  Measured with
+// SQ_LDS_BANK_CONFLICT on the Mistral-7B / Qwen2.5-72B head batches (per
+// launch): no permutation 70.8M / 210.8M conflict cycles; XOR (r & 15) 6.8M /
+// 16.8M; XOR 2 (r & 7) 1.8M / 1.9M (what the 32-byte row pad gave), so the 8
+// rows of a K read group and the 4 rows x 32 bytes of a V transpose-read
+// group land on distinct banks.  128-byte rows (head_dim 64) put two rows in
+// a bank period and take XOR 2 ((r >> 1) & 3).
 template <int D>
 __device__ __forceinline__ int chunk_slot(int r, int c) {
-  if constexpr (D == 64) return c ^ (((r >> 1) & 3) << 1);  // 128-byte rows: two per bank period
-  else return c ^ (((r & 7) << 1) | ((r >> 3) & 1));         // 256 / 512-byte rows
+  if constexpr (D == 64) return c ^ (((r >> 1) & 3) << 1);
+  else return c ^ ((r & 7) << 1);
 }
 
 template <int D, int MAXRB_>
