@@ -6,15 +6,16 @@
 // j <= i + (kv_len - qo_len); the reference always has kv_len == qo_len.
 //
 // Work decomposition.  A workgroup (4 waves) owns `bm` query positions of one
-// request and ALL `group` Q heads of one KV head: (bm / 16) x group row blocks
-// of 16 (position, head) rows, dealt to the waves round robin (at most two per
-// wave, computed together so every K / V operand read from LDS feeds both).
-// bm = 128 / group rounded down to a multiple of 16 (at least 16; 64 / group
-// for head_dim 256), so a workgroup covers 80-128 rows and every K/V byte it
-// stages serves all the heads of its group.  (8-wave workgroups over twice
-// the positions halve the staging per wave but measured 10 % slower: two
-// independent 4-wave workgroups per CU keep computing across each other's
-// barriers.)  plan() lists the tiles request
+// request and ALL `group` Q heads of one KV head: bm x group (position, head)
+// rows in position-major order, cut into row blocks of 16 rows dealt to the
+// waves round robin (three per wave for head_dim 128, two for 64, one for 256,
+// computed together so every K / V operand read from LDS feeds all of them).
+// bm = rows / group (192 rows for head_dim 128: 24 positions for group 8, 48
+// for group 4), so every K/V byte the workgroup stages serves all the heads
+// of its group.  (8-wave workgroups over twice the positions halve the
+// staging per wave but measured 10 % slower: two independent 4-wave
+// workgroups per CU keep computing across each other's barriers.)  plan()
+// lists the tiles request
 // by request (longest prompt first), each request's tiles heaviest first; the
 // grid maps tile-major, so the XCD that a KV head's workgroups land on runs
 // one request's tiles back to back and finds its K / V in L2.
@@ -46,7 +47,7 @@ constexpr int kWaitVmcnt0 = 0x0F70;
 constexpr int kBufferWord3 = 0x00020000;
 
 constexpr int kPageSize = 16;
-constexpr int kMinRows = 16;   // smallest query-position block per workgroup
+constexpr int kMinRows = 8;    // fewest query positions per workgroup (head_dim 256, group 8)
 constexpr int kKvTile = 64;    // keys per staged tile (4 pages)
 constexpr float kLazyRescale = 8.0f;
 #ifndef PREFILL_WAVES
@@ -93,24 +94,15 @@ struct PrefillHeader {
 // Waves per workgroup.
 constexpr int waves_for(int /*head_dim*/) { return 4; }
 
-// Row blocks of 16 (position, head) rows per wave: head_dim 256 one; head_dim
-// 128 three when 192 rows make 12 whole row blocks (group 1, 2, 3, 4, 6:
-// each K / V operand read from LDS then feeds three blocks -- Mistral-7B
-// heads, 32 prompts U[128, 1024]: 183 -> 170 us), else two (with group 5, 7
-// or 8 a third block would often be empty and its MFMAs wasted: group 8
-// 319 -> 378 us); head_dim 64 two.
-int row_blocks(int group, int head_dim) {
-  if (head_dim > 128) return 1;
-  if (head_dim == 128 && (192 / group) / 16 * 16 * group == 192) return 3;
-  return 2;
-}
+// Row blocks of 16 (position, head) rows per wave: three for head_dim 128
+// (each K / V operand read from LDS then feeds three blocks), two for 64, one
+// for 256.
+int row_blocks(int /*group*/, int head_dim) { return head_dim > 128 ? 1 : head_dim == 128 ? 3 : 2; }
 
-// Query positions per workgroup: bm = (16 * waves * row blocks per wave) /
-// group rounded down to a multiple of 16 (at least 16); 64 / group for
-// head_dim 256.
+// Query positions per workgroup: the workgroup's 16 * waves * row blocks rows
+// hold bm positions x group heads, bm = rows / group.
 int rows_per_tile(int group, int head_dim) {
-  const int rows = head_dim <= 128 ? 16 * waves_for(head_dim) * row_blocks(group, head_dim) : 64;
-  const int bm = (rows / group) / 16 * 16;
+  const int bm = 16 * waves_for(head_dim) * row_blocks(group, head_dim) / group;
   return bm < kMinRows ? kMinRows : bm;
 }
 
@@ -306,8 +298,11 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int g = lane >> 4, n = lane & 15;
   const int off = t.kv_len - t.qo_len;
-  const int pblocks = p.bm / 16;          // position blocks per head
-  const int nrb = pblocks * p.group;      // row blocks of the workgroup
+  // the workgroup's rows in position-major order: row R is position R / group
+  // of the tile, head R % group of this KV head's group; row block rb holds
+  // rows 16 rb .. 16 rb + 15
+  const int nrows = p.bm * p.group;
+  const int nrb = (nrows + 15) / 16;
 
 
   // ---- this wave's row blocks: rb = w, w + 4
@@ -317,8 +312,8 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
   int qpos[T::MAXRB];     // request-relative position of this lane's row n (-1: none)
   int lim[T::MAXRB];      // last key this lane's row may see (-1: none)
   int rb_hi[T::MAXRB];    // keys this row block needs (causal)
-  int head[T::MAXRB];
-  int pbk[T::MAXRB];      // position block of the row block
+  int head[T::MAXRB];     // this lane's row's Q head
+  int lpos[T::MAXRB];     // this lane's row's position within the tile (-1: none)
   int nblk = 0;
   const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.q + int64_t(t.q_begin) * p.q_st), (short)0, int(int64_t(t.q_rows) * p.q_st * 2), kBufferWord3);
@@ -327,15 +322,14 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
     const int rb = w + T::WAVES * r;
     const bool has = rb < nrb;
     nblk += has ? 1 : 0;
-    const int hg = has ? rb / pblocks : 0;
-    const int pb = has ? rb - hg * pblocks : 0;
-    head[r] = hkv * p.group + hg;
-    pbk[r] = pb;
-    const int local = pb * 16 + n;
-    const bool valid = has && local < t.q_rows;
+    const int row = rb * 16 + n;
+    const int local = row / p.group;
+    head[r] = hkv * p.group + (row - local * p.group);
+    const bool valid = has && row < nrows && local < t.q_rows;
+    lpos[r] = valid ? local : -1;
     qpos[r] = valid ? t.row0 + local : -1;
     lim[r] = !valid ? -1 : (p.causal ? min(t.kv_len - 1, qpos[r] + off) : t.kv_len - 1);
-    const int last = t.row0 + min(pb * 16 + 15, t.q_rows - 1);
+    const int last = t.row0 + min((rb * 16 + 15) / p.group, t.q_rows - 1);  // the block's last position
     rb_hi[r] = !has ? 0 : (p.causal ? min(t.kv_len, last + off + 1) : t.kv_len);
     // Q rows through a descriptor over the tile's rows: a row past the tile
     // reads out of range (zeros), so the loads are unconditional
@@ -680,8 +674,8 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
 #pragma unroll
   for (int r = 0; r < T::MAXRB; ++r) {
     if (r >= nblk) continue;
-    const int local = pbk[r] * 16 + n;
-    const bool valid = local < t.q_rows && t.q_begin + local < p.total_q;
+    const int local = lpos[r];
+    const bool valid = local >= 0 && t.q_begin + local < p.total_q;
     const int off = valid ? int((int64_t(local) * p.o_st + int64_t(head[r]) * p.o_sh) * 2) + 16 * g : 0x7ffffff0;
 #pragma unroll
     for (int q = 0; q < D / 32; ++q) {
@@ -780,12 +774,7 @@ extern "C" int mi_prefill_run(void* workspace, size_t workspace_bytes, const voi
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (head_dim) {
     case 64: hipLaunchKernelGGL((prefill_run_kernel<64, 2>), g, dim3(64 * waves_for(64)), 0, s, rp); break;
-    case 128:
-      if (row_blocks(rp.group, 128) == 3)
-        hipLaunchKernelGGL((prefill_run_kernel<128, 3>), g, dim3(64 * waves_for(128)), 0, s, rp);
-      else
-        hipLaunchKernelGGL((prefill_run_kernel<128, 2>), g, dim3(64 * waves_for(128)), 0, s, rp);
-      break;
+    case 128: hipLaunchKernelGGL((prefill_run_kernel<128, 3>), g, dim3(64 * waves_for(128)), 0, s, rp); break;
     default: hipLaunchKernelGGL((prefill_run_kernel<256, 1>), g, dim3(64 * waves_for(256)), 0, s, rp); break;
   }
   return mi::check_launch("prefill_run_kernel");

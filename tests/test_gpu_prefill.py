@@ -40,7 +40,8 @@ def _run(dev, b, qo_lens, hq, hkv, d, causal=True, seed=0):
 
 
 @pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (32, 8, 128), (28, 4, 128), (64, 8, 128),
-                                      (6, 3, 128), (8, 1, 64), (16, 4, 256)])
+                                      (6, 3, 128), (8, 1, 64), (16, 4, 256), (8, 1, 256), (10, 2, 256),
+                                      (40, 8, 128)])
 @pytest.mark.parametrize("L", [1, 5, 64, 100, 300])
 def test_single_request_causal(dev, parity, hq, hkv, d, L):
     b = make_paged_batch([L], hq, hkv, d, seed=L + d)
