@@ -486,15 +486,20 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
   constexpr int RK = D / 16, VC = D / 8;
   const int split = u / p.hkv - item_base;
   const bool appender = ROPE && split == nsplit - 1 && npg > 0;
-  u32x4_t cs_v, k_lo, k_hi, v_new;
+  u32x4_t c_v, s_v, k_lo, k_hi, v_new;
   int new_page = -1;
   if constexpr (ROPE) {
     // the decode position kv_len - 1 is the RoPE row: no load on the way
     const int rp = min(max(mi::read_lane_i(iv, kItemKvLen) - 1, 0), p.table_rows - 1);
+    // one descriptor per table (a per-lane table pointer would make the
+    // descriptor divergent); lanes outside a table's range read zeros
     const bool is_cos = lane < VC, is_sin = lane >= VC && lane < 2 * VC;
-    const uint16_t* tab = (is_cos ? p.cos : p.sin) + int64_t(rp) * D;
-    const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc((void*)tab, (short)0, D * 2, kBufferWord3);
-    cs_v = __builtin_amdgcn_raw_buffer_load_b128(rt, is_cos ? 16 * lane : is_sin ? 16 * (lane - VC) : 0x7ffffff0, 0, 0);
+    const __amdgpu_buffer_rsrc_t rcos =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(p.cos + int64_t(rp) * D), (short)0, D * 2, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rsin =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(p.sin + int64_t(rp) * D), (short)0, D * 2, kBufferWord3);
+    c_v = __builtin_amdgcn_raw_buffer_load_b128(rcos, is_cos ? 16 * lane : 0x7ffffff0, 0, 0);
+    s_v = __builtin_amdgcn_raw_buffer_load_b128(rsin, is_sin ? 16 * (lane - VC) : 0x7ffffff0, 0, 0);
     // this head's K row and V row in the qkv row (V heads follow the K heads)
     const char* krow = reinterpret_cast<const char*>(p.q + int64_t(b) * p.q_sb) + p.k_col_bytes + hkv * D * 2;
     const __amdgpu_buffer_rsrc_t rkv = __builtin_amdgcn_make_buffer_rsrc(
@@ -585,7 +590,11 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
   // in the staging slot of its page, and is written to the pool at the end
   auto rotate = [&]() {
     if constexpr (ROPE) {
-      if (lane < 2 * VC) lds_store16(rx + 16 * lane, cs_v);  // cos row, then sin row
+      // cos row, then sin row.  The load registers are loop-invariant: the
+      // opaque step keeps the compiler from merging them (a select) before
+      // the first page loads, which would wait for these loads there.
+      __asm__ volatile("" : "+v"(c_v), "+v"(s_v));
+      if (lane < 2 * VC) lds_store16(rx + 16 * lane, lane < VC ? c_v : s_v);
       const lds_t* cr = rx;
       const lds_t* sr = rx + D * 2;
 #pragma unroll
@@ -600,6 +609,11 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
         qb[s + T::KSTEPS / 2] = __builtin_bit_cast(mi::bf16x8_t, o2);
       }
       if (appender) {
+        // k_lo / k_hi likewise: without the opaque step the compiler hoisted
+        // their bf16 unpacking above the first page loads, and every wave
+        // then waited for its Q, cos / sin and new-row loads before issuing a
+        // page (Mistral-7B B=32 fused launch +0.8 us)
+        __asm__ volatile("" : "+v"(k_lo), "+v"(k_hi));
         if (lane < RK) {
           uint4 o1, o2;
           mi::rope8(__builtin_bit_cast(uint4, k_lo), __builtin_bit_cast(uint4, k_hi),
@@ -809,7 +823,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 128
   __shared__ __attribute__((aligned(16))) char slot[W * T::SLOT + (ROPE ? W * T::RX : 0)];
   lds_t* lds = (lds_t*)slot;
   lds_t* rx = lds + W * T::SLOT + (ROPE ? int(threadIdx.x >> 6) * T::RX : 0);  // this wave's RoPE rows
-  int u = int(blockIdx.x) * W + int(threadIdx.x >> 6);
+  // the unit is wave-uniform (readfirstlane): its head, request and row
+  // pointers then live in scalar registers, and the buffer descriptors built
+  // from them need no per-lane (waterfall) loops
+  int u = int(blockIdx.x) * W + (W == 1 ? 0 : __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6)));
   // The first item is read before the unit count is known (in bounds either
   // way), so the reads are in flight together.
   int iv = load_item_word(p, u);
