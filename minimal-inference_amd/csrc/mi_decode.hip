@@ -193,6 +193,7 @@ typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4_v;
 typedef __attribute__((ext_vector_type(8))) float f32x8_v;
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_v;
 typedef __attribute__((ext_vector_type(8))) short s16x8_t;
+typedef __attribute__((ext_vector_type(2))) float f32x2_v;
 
 // Max / sum of x and its value in lane ^ 16 (resp. lane ^ 32), with the
 // gfx950 lane-swap instructions: swapping x with itself leaves x in one
@@ -444,7 +445,7 @@ __device__ __forceinline__ void publish_merge(const RunParams& p, int u, int b, 
 // pool's stale slot and writes them to the slot -- the decode step's RoPE
 // (model.py:169-170) and append (model.py:203-216) done by the attention
 // launch (model.py:235) with the same bf16 arithmetic as rope_append_kernel.
-template <int D, int G, int W, int NB, bool ROPE>
+template <int D, int G, int W, int S, int NB, bool ROPE>
 __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, lds_t* wg_lds, lds_t* rx) {
   using T = DecodeTraits<D, G>;
   using Regs = PageRegs<D, G>;
@@ -522,21 +523,31 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
   const int tok_bytes = p.hkv * D * 2;
   const int kv_bytes = kPageSize * tok_bytes;
   const int page_bytes = 2 * kv_bytes;
-  const int w = (W == 1) ? 0 : __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  // wave wv of the workgroup: head w of its W heads, lane group sg of S
+  const int wv = (W * S == 1) ? 0 : __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const int w = wv % W, sg = wv / W;
   const int row0 = w * RPW;
   const int lrow = lane / LPR, lbyte = (lane % LPR) * 16;
   const int lhead = lbyte / (D * 2), lchunk = (lbyte % (D * 2)) / 16;
   const int voff = lrow * tok_bytes + (hkv - w) * D * 2 + lbyte;
-  lds_t* const lds = wg_lds + w * T::SLOT;  // this wave's head
-  lds_t* const stage_lds = wg_lds + lhead * T::SLOT;  // the head of this lane's loaded bytes
+  lds_t* const lds = wg_lds + (sg * W + w) * T::SLOT;  // this wave's head
+  lds_t* const stage_lds = wg_lds + (sg * W + lhead) * T::SLOT;  // the head of this lane's loaded bytes
 
   int pidv = iv;  // page ids of the current group, lane k = page k of the group
 
   auto page_id = [&](int k) { return __builtin_amdgcn_readlane(pidv, k & 63); };
   auto page_ok = [&](int k, int pg, int gsize) { return k < gsize && pg >= 0 && pg < p.num_pages; };
+  // With S = 2 lane groups, a unit's pages are dealt to them pair by pair:
+  // page k of lane group sg's sequence is page act(k) of the id group, and
+  // both groups walk sequences of the same length vsize(gsize) (a missing
+  // pair loads through a size-0 descriptor and is masked), so every wave of
+  // the workgroup reaches the same barriers.
+  auto act = [&](int k) { return S == 1 ? k : 4 * (k >> 1) + 2 * sg + (k & 1); };
+  auto vsize = [&](int gs) { return S == 1 ? gs : 2 * (((gs + 1) / 2 + 1) / 2); };
   auto issue = [&](Regs& r, int k, int gsize) {
-    const int pg = page_id(k);
-    const bool ok = page_ok(k, pg, gsize);
+    const int a = act(k);
+    const int pg = page_id(a);
+    const bool ok = page_ok(a, pg, gsize);
     const char* base = ok ? p.pool + int64_t(pg) * page_bytes : p.pool;
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, ok ? page_bytes : 0, kBufferWord3);
@@ -735,12 +746,16 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
 #pragma unroll
     for (int s = 0; s < NB; ++s) issue(buf[s], s, gsize);
     auto page_valid = [&](int k) {
-      const int valid = (g_start + k == npg - 1) ? last_valid : kPageSize;
-      return page_ok(k, page_id(k), gsize) ? valid : 0;
+      const int a = act(k);
+      const int valid = (g_start + a == npg - 1) ? last_valid : kPageSize;
+      return page_ok(a, page_id(a), gsize) ? valid : 0;
     };
     // the slot of the pair (k, k + 1) that holds the new token, for its appender
-    auto inj_slot = [&](int k) { return !appender ? -1 : g_start + k == npg - 1 ? 0 : g_start + k + 1 == npg - 1 ? 1 : -1; };
-    const int full = gsize / NB;
+    auto inj_slot = [&](int k) {
+      return !appender ? -1 : g_start + act(k) == npg - 1 ? 0 : g_start + act(k + 1) == npg - 1 ? 1 : -1;
+    };
+    const int vs = vsize(gsize);
+    const int full = vs / NB;
     for (int it = 0; it < full; ++it) {
 #pragma unroll
       for (int s = 0; s < NB; s += 2) {
@@ -753,7 +768,7 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
     }
     // the last rem (< NB) pages; a pair's second page past the group's end
     // was loaded through a size-0 descriptor (zeros) and is fully masked
-    const int rem = gsize - full * NB;
+    const int rem = vs - full * NB;
 #pragma unroll
     for (int s = 0; s < NB - 1; s += 2)
       if (s < rem) consume2(buf[s], page_valid(full * NB + s), buf[s + 1],
@@ -772,7 +787,7 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
   // ---- the append: the new K / V row from `rx` to its slot, one 16-byte
   // chunk per lane (a page id outside the pool writes nothing)
   if constexpr (ROPE) {
-    if (appender) {
+    if (appender && sg == 0) {
       const bool ok = new_page >= 0 && new_page < p.num_pages;
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
           (void*)(ok ? p.pool + int64_t(new_page) * page_bytes : p.pool), (short)0, ok ? page_bytes : 0,
@@ -784,6 +799,41 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
       __builtin_amdgcn_raw_buffer_store_b128(x, rs, kl ? row_off + 16 * c : vl ? kv_bytes + row_off + 16 * c : 0x7ffffff0,
                                              0, 0);
     }
+  }
+
+  // ---- lane group 1 hands its state (O accumulators, m, l) to lane group 0
+  // through its own LDS slot, free after the last step's barrier; the second
+  // barrier keeps the slot from being restaged before group 0 has read it
+  if constexpr (S == 2) {
+    lds_t* const xs = wg_lds + (W + w) * T::SLOT;
+    static_assert(T::NT * 1024 + 512 <= T::SLOT, "hand-off fits the slot");
+    if (sg == 1) {
+#pragma unroll
+      for (int t = 0; t < T::NT; ++t) lds_store16(xs + (t * 64 + lane) * 16, __builtin_bit_cast(u32x4_t, acc[t]));
+      *(__attribute__((address_space(3))) f32x2_v*)(xs + T::NT * 1024 + lane * 8) = f32x2_v{m_run, l_run};
+    }
+    __syncthreads();  // every wave of the workgroup, whatever W
+    if (sg == 0) {
+      mi::f32x4_t acc1[T::NT];
+#pragma unroll
+      for (int t = 0; t < T::NT; ++t) acc1[t] = __builtin_bit_cast(mi::f32x4_t, lds_load16(xs + (t * 64 + lane) * 16));
+      const f32x2_v ml1 = *(const __attribute__((address_space(3))) f32x2_v*)(xs + T::NT * 1024 + lane * 8);
+      // m of head j (the same in every lane of head j); a group that saw no
+      // token has m = -inf, O = 0, l = 0 and weight 0
+      const float mm = fmaxf(m_run, ml1.x);
+      const float f0 = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - mm);
+      const float f1 = (ml1.x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ml1.x - mm);
+      l_run = l_run * f0 + ml1.y * f1;
+      m_run = mm;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a0 = mi::lane_shuffle(f0, 4 * g + i), a1 = mi::lane_shuffle(f1, 4 * g + i);
+#pragma unroll
+        for (int t = 0; t < T::NT; ++t) acc[t][i] = acc[t][i] * a0 + acc1[t][i] * a1;
+      }
+    }
+    __syncthreads();
+    if (sg == 1) return;
   }
 
   // ---- per-head denominators; O rows are heads 4g + i
@@ -816,23 +866,23 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
 // head_dim <= 128: registers capped at 256 per wave, so at least two waves
 // share a SIMD (the plan's 6 units per CU fit).  head_dim 256 needs the full
 // register file.
-template <int D, int G, int W, bool ROPE>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 128 ? MI_DECODE_WAVES : 1))) void decode_run_kernel(
+template <int D, int G, int W, int S, bool ROPE>
+__global__ __launch_bounds__(64 * W * S) __attribute__((amdgpu_waves_per_eu(D <= 128 ? MI_DECODE_WAVES : 1))) void decode_run_kernel(
     RunParams p) {
   using T = DecodeTraits<D, G>;
-  __shared__ __attribute__((aligned(16))) char slot[W * T::SLOT + (ROPE ? W * T::RX : 0)];
+  __shared__ __attribute__((aligned(16))) char slot[W * S * T::SLOT + (ROPE ? W * S * T::RX : 0)];
   lds_t* lds = (lds_t*)slot;
-  lds_t* rx = lds + W * T::SLOT + (ROPE ? int(threadIdx.x >> 6) * T::RX : 0);  // this wave's RoPE rows
+  lds_t* rx = lds + W * S * T::SLOT + (ROPE ? int(threadIdx.x >> 6) * T::RX : 0);  // this wave's RoPE rows
   // the unit is wave-uniform (readfirstlane): its head, request and row
   // pointers then live in scalar registers, and the buffer descriptors built
   // from them need no per-lane (waterfall) loops
-  int u = int(blockIdx.x) * W + (W == 1 ? 0 : __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6)));
+  int u = int(blockIdx.x) * W + (W == 1 ? 0 : __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6) % W));
   // The first item is read before the unit count is known (in bounds either
   // way), so the reads are in flight together.
   int iv = load_item_word(p, u);
   const int num_units = p.header->num_units;
   while (u < num_units) {
-    decode_unit<D, G, W, T::NB, ROPE>(p, u, iv, lds, rx);
+    decode_unit<D, G, W, S, T::NB, ROPE>(p, u, iv, lds, rx);
     u += int(gridDim.x) * W;
     if (u < num_units) iv = load_item_word(p, u);
   }
@@ -840,17 +890,17 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 128
 
 typedef void (*RunKernel)(RunParams);
 
-template <int D, int W, bool ROPE>
+template <int D, int W, int S, bool ROPE>
 RunKernel pick_group(int g) {
   switch (g) {
-    case 1: return decode_run_kernel<D, 1, W, ROPE>;
-    case 2: return decode_run_kernel<D, 2, W, ROPE>;
-    case 3: return decode_run_kernel<D, 3, W, ROPE>;
-    case 4: return decode_run_kernel<D, 4, W, ROPE>;
-    case 5: return decode_run_kernel<D, 5, W, ROPE>;
-    case 6: return decode_run_kernel<D, 6, W, ROPE>;
-    case 7: return decode_run_kernel<D, 7, W, ROPE>;
-    case 8: return decode_run_kernel<D, 8, W, ROPE>;
+    case 1: return decode_run_kernel<D, 1, W, S, ROPE>;
+    case 2: return decode_run_kernel<D, 2, W, S, ROPE>;
+    case 3: return decode_run_kernel<D, 3, W, S, ROPE>;
+    case 4: return decode_run_kernel<D, 4, W, S, ROPE>;
+    case 5: return decode_run_kernel<D, 5, W, S, ROPE>;
+    case 6: return decode_run_kernel<D, 6, W, S, ROPE>;
+    case 7: return decode_run_kernel<D, 7, W, S, ROPE>;
+    case 8: return decode_run_kernel<D, 8, W, S, ROPE>;
     default: return nullptr;
   }
 }
@@ -860,18 +910,42 @@ RunKernel pick_group(int g) {
 int waves_per_group(int head_dim, int hkv) { return (head_dim <= 128 && hkv % 2 == 0) ? 2 : 1; }
 
 template <bool ROPE>
-RunKernel pick_kernel(int head_dim, int group, int waves) {
+RunKernel pick_kernel(int head_dim, int group, int waves, int lanes) {
   switch (head_dim) {
-    case 64: return waves == 2 ? pick_group<64, 2, ROPE>(group) : pick_group<64, 1, ROPE>(group);
-    case 128: return waves == 2 ? pick_group<128, 2, ROPE>(group) : pick_group<128, 1, ROPE>(group);
-    case 256: return waves == 1 ? pick_group<256, 1, ROPE>(group) : nullptr;
+    case 64:
+      if (lanes == 2) return waves == 2 ? pick_group<64, 2, 2, ROPE>(group) : pick_group<64, 1, 2, ROPE>(group);
+      return waves == 2 ? pick_group<64, 2, 1, ROPE>(group) : pick_group<64, 1, 1, ROPE>(group);
+    case 128: return waves == 2 ? pick_group<128, 2, 1, ROPE>(group) : pick_group<128, 1, 1, ROPE>(group);
+    case 256: return waves == 1 ? pick_group<256, 1, 1, ROPE>(group) : nullptr;
     default: return nullptr;
   }
 }
 
+// Units the plan aims at: one resident round of kUnitsPerCU per CU, but at
+// most ~MI_DECODE_MERGE_BUDGET / group splits per (request, KV head) on
+// average -- the merge's cost grows with splits x group (Qwen2.5-7B, group
+// 7: 4 units per CU instead of 6 took ~1 us off) -- and at least two per CU.
+int plan_target_units(int batch, int hq, int hkv) {
+  const int group = hq / hkv;
+  const long long cap = (long long)(MI_DECODE_MERGE_BUDGET / group) * batch * hkv;
+  const int round = mi::num_cus() * kUnitsPerCU;
+  return int(cap < round ? (cap > mi::num_cus() * 2 ? cap : mi::num_cus() * 2) : round);
+}
+
+// Lane groups per unit: two when the plan aims at no more than three units
+// per CU at head_dim 64 -- too few waves to overlap each wave's per-step
+// chain (Qwen2.5-0.5B heads, B=32: one two-wave workgroup per CU, each page
+// pair 0.92 us of which 0.06 us waiting for its loads) -- so each unit's
+// pages are split over two waves per head and merged in LDS.  Else one.
+int lane_groups(int head_dim, int batch, int hq, int hkv) {
+  return (head_dim == 64 && plan_target_units(batch, hq, hkv) <= mi::num_cus() * 3) ? 2 : 1;
+}
+
 // Workgroups of the run launch: one resident round of units (capped by the
-// workspace), W units each.  plan() and run() both use it.
-int run_grid(int max_units, int waves) { return max(1, min(max_units, mi::num_cus() * kUnitsPerCU) / waves); }
+// workspace), W units each (kUnitsPerCU per CU, or 3 with two lane groups).
+int run_grid(int max_units, int waves, int lanes) {
+  return max(1, min(max_units, mi::num_cus() * (lanes == 2 ? 3 : kUnitsPerCU)) / waves);
+}
 
 int check_shape(const char* who, int batch, int hq, int hkv, int head_dim, int page_size) {
   if (batch < 0 || hq <= 0 || hkv <= 0)
@@ -880,7 +954,7 @@ int check_shape(const char* who, int batch, int hq, int hkv, int head_dim, int p
     return mi::fail(MI_ERR_INVALID, "%s: num_qo_heads %d not a multiple of num_kv_heads %d", who, hq, hkv);
   if (page_size != kPageSize)
     return mi::fail(MI_ERR_UNSUPPORTED, "%s: page_size %d (built for 16)", who, page_size);
-  if (!pick_kernel<false>(head_dim, hq / hkv, waves_per_group(head_dim, hkv)))
+  if (!pick_kernel<false>(head_dim, hq / hkv, waves_per_group(head_dim, hkv), 1))
     return mi::fail(MI_ERR_UNSUPPORTED, "%s: head_dim %d / group %d not built (head_dim 64/128/256, group 1..8)",
                     who, head_dim, hq / hkv);
   return MI_OK;
@@ -909,15 +983,7 @@ int mi::dplan::plan_setup(const char* who, void* workspace, size_t workspace_byt
   char* ws = static_cast<char*>(workspace);
   pp->batch = batch;
   pp->hkv = hkv;
-  // One resident round of units, but at most ~40 / group splits per
-  // (request, KV head) on average: the merge's cost grows with splits x
-  // group (Qwen2.5-7B, group 7: 4 units per CU instead of 6 took ~1 us off).
-  {
-    const int group = hq / hkv;
-    const long long cap = (long long)(MI_DECODE_MERGE_BUDGET / group) * batch * hkv;
-    const int round = mi::num_cus() * kUnitsPerCU;
-    pp->target_units = int(cap < round ? (cap > mi::num_cus() * 2 ? cap : mi::num_cus() * 2) : round);
-  }
+  pp->target_units = plan_target_units(batch, hq, hkv);
   pp->max_items = L.max_items;
   pp->header = reinterpret_cast<DecodeHeader*>(ws);
   pp->items = reinterpret_cast<DecodeItem*>(ws + L.items);
@@ -975,9 +1041,11 @@ int launch_run(const char* who, bool rope, RunParams rp, void* workspace, size_t
   const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf(float(head_dim));
   rp.scale_log2 = scale * mi::kLog2e;
   const int waves = waves_per_group(head_dim, num_kv_heads);
-  RunKernel k = rope ? pick_kernel<true>(head_dim, num_qo_heads / num_kv_heads, waves)
-                     : pick_kernel<false>(head_dim, num_qo_heads / num_kv_heads, waves);
-  hipLaunchKernelGGL(k, dim3(run_grid(max_units, waves)), dim3(64 * waves), 0, static_cast<hipStream_t>(stream), rp);
+  const int lanes = lane_groups(head_dim, batch_size, num_qo_heads, num_kv_heads);
+  RunKernel k = rope ? pick_kernel<true>(head_dim, num_qo_heads / num_kv_heads, waves, lanes)
+                     : pick_kernel<false>(head_dim, num_qo_heads / num_kv_heads, waves, lanes);
+  hipLaunchKernelGGL(k, dim3(run_grid(max_units, waves, lanes)), dim3(64 * waves * lanes), 0,
+                     static_cast<hipStream_t>(stream), rp);
   return mi::check_launch("decode_run_kernel");
 }
 

@@ -62,6 +62,8 @@ def test_config1_qwen05_heads(dev, parity):
     (4, 1, 64),     # one KV head, head_dim 64
 ])
 def test_shapes_ragged(dev, parity, hq, hkv, d):
+    # eight requests: the head_dim 64 shapes get two lane groups per unit
+    # (the plan aims at two units per CU), the others one
     lens = [1, 15, 16, 17, 33, 100, 257, 700]
     b = make_paged_batch(lens, hq, hkv, d, seed=hq * 7 + d)
     parity(_decode(dev, b, hq, hkv, d), _ref(b))
@@ -234,7 +236,8 @@ def test_stale_rows_past_the_end_are_not_read(dev, parity, hq, hkv, d):
 
 @pytest.mark.parametrize("B,hq,hkv,d,max_ctx", [
     (700, 32, 8, 128, 80),   # units > one resident round: the run's grid-stride rounds
-    (1100, 8, 2, 64, 40),    # more requests than the plan's 1024-thread scan takes at once
+    (1100, 8, 2, 64, 40),    # more requests than the plan's 1024-thread scan takes at once; head_dim 64
+                             # with a full round of units, so one lane group per unit
 ])
 def test_large_batches(dev, parity, B, hq, hkv, d, max_ctx):
     g = torch.Generator().manual_seed(B)
@@ -246,7 +249,7 @@ def test_large_batches(dev, parity, B, hq, hkv, d, max_ctx):
 @pytest.mark.parametrize("hq,hkv,d,lo,hi", [
     (32, 8, 128, 153, 1049),    # Mistral-7B decode batch: items of 6-7 pages
     (64, 8, 128, 512, 4096),    # Qwen2.5-72B heads: items of 16-29 pages, some past the 24 inline page ids
-    (14, 2, 64, 512, 4096),     # Qwen2.5-0.5B heads: head_dim 64, four pages in flight
+    (14, 2, 64, 512, 4096),     # Qwen2.5-0.5B heads: head_dim 64, two lane groups merged in LDS
 ])
 def test_repeated_runs_are_bit_identical(dev, parity, hq, hkv, d, lo, hi):
     """Units finish in a different order on every launch and whichever split
