@@ -537,13 +537,13 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
 
   auto page_id = [&](int k) { return __builtin_amdgcn_readlane(pidv, k & 63); };
   auto page_ok = [&](int k, int pg, int gsize) { return k < gsize && pg >= 0 && pg < p.num_pages; };
-  // With S = 2 lane groups, a unit's pages are dealt to them pair by pair:
+  // With S > 1 lane groups, a unit's pages are dealt to them pair by pair:
   // page k of lane group sg's sequence is page act(k) of the id group, and
-  // both groups walk sequences of the same length vsize(gsize) (a missing
+  // all groups walk sequences of the same length vsize(gsize) (a missing
   // pair loads through a size-0 descriptor and is masked), so every wave of
   // the workgroup reaches the same barriers.
-  auto act = [&](int k) { return S == 1 ? k : 4 * (k >> 1) + 2 * sg + (k & 1); };
-  auto vsize = [&](int gs) { return S == 1 ? gs : 2 * (((gs + 1) / 2 + 1) / 2); };
+  auto act = [&](int k) { return S == 1 ? k : 2 * S * (k >> 1) + 2 * sg + (k & 1); };
+  auto vsize = [&](int gs) { return S == 1 ? gs : 2 * (((gs + 1) / 2 + S - 1) / S); };
   auto issue = [&](Regs& r, int k, int gsize) {
     const int a = act(k);
     const int pg = page_id(a);
@@ -801,39 +801,44 @@ __device__ __forceinline__ void decode_unit(const RunParams& p, int u, int iv, l
     }
   }
 
-  // ---- lane group 1 hands its state (O accumulators, m, l) to lane group 0
-  // through its own LDS slot, free after the last step's barrier; the second
-  // barrier keeps the slot from being restaged before group 0 has read it
-  if constexpr (S == 2) {
-    lds_t* const xs = wg_lds + (W + w) * T::SLOT;
+  // ---- lane groups 1 .. S-1 hand their state (O accumulators, m, l) to
+  // lane group 0 through their own LDS slots, free after the last step's
+  // barrier; the second barrier keeps the slots from being restaged before
+  // group 0 has read them
+  if constexpr (S > 1) {
     static_assert(T::NT * 1024 + 512 <= T::SLOT, "hand-off fits the slot");
-    if (sg == 1) {
+    if (sg > 0) {
+      lds_t* const xs = wg_lds + (sg * W + w) * T::SLOT;
 #pragma unroll
       for (int t = 0; t < T::NT; ++t) lds_store16(xs + (t * 64 + lane) * 16, __builtin_bit_cast(u32x4_t, acc[t]));
       *(__attribute__((address_space(3))) f32x2_v*)(xs + T::NT * 1024 + lane * 8) = f32x2_v{m_run, l_run};
     }
     __syncthreads();  // every wave of the workgroup, whatever W
     if (sg == 0) {
-      mi::f32x4_t acc1[T::NT];
 #pragma unroll
-      for (int t = 0; t < T::NT; ++t) acc1[t] = __builtin_bit_cast(mi::f32x4_t, lds_load16(xs + (t * 64 + lane) * 16));
-      const f32x2_v ml1 = *(const __attribute__((address_space(3))) f32x2_v*)(xs + T::NT * 1024 + lane * 8);
-      // m of head j (the same in every lane of head j); a group that saw no
-      // token has m = -inf, O = 0, l = 0 and weight 0
-      const float mm = fmaxf(m_run, ml1.x);
-      const float f0 = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - mm);
-      const float f1 = (ml1.x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ml1.x - mm);
-      l_run = l_run * f0 + ml1.y * f1;
-      m_run = mm;
+      for (int o = 1; o < S; ++o) {
+        const lds_t* const xs = wg_lds + (o * W + w) * T::SLOT;
+        mi::f32x4_t acc1[T::NT];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float a0 = mi::lane_shuffle(f0, 4 * g + i), a1 = mi::lane_shuffle(f1, 4 * g + i);
+        for (int t = 0; t < T::NT; ++t) acc1[t] = __builtin_bit_cast(mi::f32x4_t, lds_load16(xs + (t * 64 + lane) * 16));
+        const f32x2_v ml1 = *(const __attribute__((address_space(3))) f32x2_v*)(xs + T::NT * 1024 + lane * 8);
+        // m of head j (the same in every lane of head j); a group that saw
+        // no token has m = -inf, O = 0, l = 0 and weight 0
+        const float mm = fmaxf(m_run, ml1.x);
+        const float f0 = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - mm);
+        const float f1 = (ml1.x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ml1.x - mm);
+        l_run = l_run * f0 + ml1.y * f1;
+        m_run = mm;
 #pragma unroll
-        for (int t = 0; t < T::NT; ++t) acc[t][i] = acc[t][i] * a0 + acc1[t][i] * a1;
+        for (int i = 0; i < 4; ++i) {
+          const float a0 = mi::lane_shuffle(f0, 4 * g + i), a1 = mi::lane_shuffle(f1, 4 * g + i);
+#pragma unroll
+          for (int t = 0; t < T::NT; ++t) acc[t][i] = acc[t][i] * a0 + acc1[t][i] * a1;
+        }
       }
     }
     __syncthreads();
-    if (sg == 1) return;
+    if (sg > 0) return;
   }
 
   // ---- per-head denominators; O rows are heads 4g + i
