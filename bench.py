@@ -1023,7 +1023,7 @@ def mistral_leg(args, dev, with_cpu: bool) -> dict:
                    "parallelism": "single GPU"},
         "decode_tok_s_one_step_per_round_trip": round(toks_single, 2),
         "decode_attn_kernel": "the decode step's attention launch: RoPE of q and k, the new K/V appended, "
-                              "split-K paged attention (mi_decode_rope_append_run, decode_run_kernel<128, 4, 2, "
+                              "split-K paged attention (mi_decode_rope_append_run, decode_run_kernel<128, 4, 2, 1, "
                               "true>)",
         "decode_attn_us": round(attn_us, 3),
         "decode_attn_gbps": round(achieved, 1),
