@@ -524,7 +524,9 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
       // P V part, and the arbiter issues this wave's MFMAs first while that
       // VALU work fills the gaps (Qwen2.5-72B / Qwen2.5-7B head batches
       // -1.9..-2.2 / -1.1..-1.5 % over three boxes, Mistral-7B heads
-      // -1.2..+0.9 %; around the P V MFMAs as well: no better)
+      // -1.2..+0.9 %; around the P V MFMAs as well: no better; the reverse
+      // -- priority over the softmax instead -- gains the same: what helps is
+      // that the two workgroups' waves on a SIMD stop moving in step)
       __builtin_amdgcn_s_setprio(1);
       if (full) scores(std::false_type{});
       else scores(std::true_type{});
