@@ -84,6 +84,16 @@ def test_long_context_many_splits(dev, parity, ctx):
     parity(_decode(dev, b, 28, 4, 128), _ref(b))
 
 
+@pytest.mark.parametrize("lens", [[16384], [3000, 1, 47, 2049], [33] * 7])
+def test_head_dim_64_lane_groups(dev, parity, lens):
+    """Head_dim 64 with few requests: two lane groups per unit deal the
+    unit's page pairs alternately and merge in LDS.  Long units span several
+    64-page id groups; odd pair counts leave one group a masked pair; a
+    one-page request gives one group no page at all; ragged sets mix them."""
+    b = make_paged_batch(lens, 14, 2, 64, seed=len(lens) * 31 + lens[0])
+    parity(_decode(dev, b, 14, 2, 64), _ref(b))
+
+
 def test_empty_request_gives_zero(dev, parity):
     b = make_paged_batch([0, 40], 8, 2, 64, seed=5)
     out = _decode(dev, b, 8, 2, 64)
