@@ -56,12 +56,14 @@ def test_ragged_batch(dev, parity):
     parity(out, ref)
 
 
-def test_kv_longer_than_q_bottom_right_causal(dev, parity):
-    """Chunked-prefill shape: the last qo_len of kv_len tokens are queries."""
+@pytest.mark.parametrize("hq,hkv,d", [(28, 4, 128), (14, 2, 64), (64, 8, 128), (16, 4, 256)])
+def test_kv_longer_than_q_bottom_right_causal(dev, parity, hq, hkv, d):
+    """Chunked-prefill shape: the last qo_len of kv_len tokens are queries
+    (row blocks whose diagonal starts mid-tile, at every head_dim and group 8)."""
     kv_lens = [100, 260, 33]
     qo_lens = [20, 64, 33]
-    b = make_paged_batch(kv_lens, 28, 4, 128, seed=4)
-    out, ref = _run(dev, b, qo_lens, 28, 4, 128, seed=4)
+    b = make_paged_batch(kv_lens, hq, hkv, d, seed=4)
+    out, ref = _run(dev, b, qo_lens, hq, hkv, d, seed=4)
     parity(out, ref)
 
 
