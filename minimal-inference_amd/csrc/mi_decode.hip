@@ -878,18 +878,30 @@ __global__ __launch_bounds__(64 * W * S) __attribute__((amdgpu_waves_per_eu(D <=
   __shared__ __attribute__((aligned(16))) char slot[W * S * T::SLOT + (ROPE ? W * S * T::RX : 0)];
   lds_t* lds = (lds_t*)slot;
   lds_t* rx = lds + W * S * T::SLOT + (ROPE ? int(threadIdx.x >> 6) * T::RX : 0);  // this wave's RoPE rows
+  // Every argument is read from the argument segment at once, up front:
+  // left to the compiler, some of these reads came after the plan's header
+  // and item loads, each one more round trip before the first page load.
+  __asm__ volatile("" ::"s"(p.header), "s"(p.items), "s"(p.q), "s"(p.pool), "s"(p.cos), "s"(p.sin), "s"(p.q_sb),
+                   "s"(p.q_sh), "s"(p.num_pages), "s"(p.hkv), "s"(p.max_items), "s"(p.table_rows),
+                   "s"(p.k_col_bytes), "s"(p.counters), "s"(p.pml), "s"(p.po), "s"(p.out), "s"(p.o_sb), "s"(p.o_sh),
+                   "s"(p.indices), "s"(p.scale_log2), "s"(p.pml_bytes), "s"(p.po_bytes));
   // the unit is wave-uniform (readfirstlane): its head, request and row
   // pointers then live in scalar registers, and the buffer descriptors built
   // from them need no per-lane (waterfall) loops
   int u = int(blockIdx.x) * W + (W == 1 ? 0 : __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6) % W));
   // The first item is read before the unit count is known (in bounds either
-  // way), so the reads are in flight together.
+  // way), so the reads are in flight together.  The first check reads the
+  // item as well (a split count is never negative): with the count alone the
+  // compiler sank the item load below it, one more round trip before the
+  // first page load (fused launch ~1 % slower on every decode shape).
   int iv = load_item_word(p, u);
   const int num_units = p.header->num_units;
-  while (u < num_units) {
+  if (!((u < num_units) & (mi::read_lane_i(iv, kItemNsplit) >= 0))) return;
+  while (true) {
     decode_unit<D, G, W, S, T::NB, ROPE>(p, u, iv, lds, rx);
     u += int(gridDim.x) * W;
-    if (u < num_units) iv = load_item_word(p, u);
+    if (u >= num_units) break;
+    iv = load_item_word(p, u);
   }
 }
 
