@@ -227,6 +227,27 @@ def test_golden_fixture_config1(dev, parity):
     parity(out, t["out_fp32"])
 
 
+@pytest.mark.parametrize("fill", ["ones", "random", "larger_plan"])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64), (6, 3, 128)])
+def test_work_items_past_the_plan_are_ignored(dev, parity, fill, hq, hkv, d):
+    """Every wave of the run reads its first work item before it knows the
+    plan's unit count; the items past that count hold whatever the workspace
+    held (all bits set, random bytes, or a larger earlier plan's items) and
+    must not be used.  A small batch leaves most of the grid past the count."""
+    from minimal_inference_amd.decode import BatchDecodeWithPagedKVCacheWrapper
+
+    ws = torch.empty(128 << 20, dtype=torch.uint8, device=dev)
+    if fill == "ones":
+        ws.fill_(0xFF)
+    elif fill == "random":
+        ws.random_(0, 256, generator=torch.Generator(device=dev).manual_seed(7))
+    w = BatchDecodeWithPagedKVCacheWrapper(ws, kv_layout="NHD")
+    if fill == "larger_plan":  # its items stay in the workspace past the small plan's
+        _decode(dev, make_paged_batch([400] * 40, hq, hkv, d, seed=31), hq, hkv, d, w=w)
+    b = make_paged_batch([33, 1, 260], hq, hkv, d, seed=32)
+    parity(_decode(dev, b, hq, hkv, d, w=w), _ref(b))
+
+
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64), (6, 3, 128)])
 def test_stale_rows_past_the_end_are_not_read(dev, parity, hq, hkv, d):
     """NaN in every pool row past each request's length on its last page."""
