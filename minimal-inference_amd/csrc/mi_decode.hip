@@ -31,7 +31,8 @@
 // device-coherent (sc1) 16-byte stores, wait for them, and bump a
 // per-(request, KV head) counter; the unit that sees the count reach
 // nsplit-1 reads the partials back (16 bytes per lane, eight splits per
-// round trip), merges them, and resets the counter.  No agent-scope fence
+// round trip -- sixteen at head_dim 64, whose next eight splits' rows load
+// with the first eight), merges them, and resets the counter.  No agent-scope fence
 // (and so no whole-L2 writeback / invalidate) is executed, and run() is one
 // launch with no memset.
 #include <math.h>
@@ -348,8 +349,14 @@ __device__ __forceinline__ void publish_merge(const RunParams& p, int u, int b, 
       for (int a = 0; a < A; ++a)
         ml[a][c] = __builtin_amdgcn_raw_buffer_load_b64(rml, (us * G + min(a * R + hg, G - 1)) * 8, 0, CP);
     }
-    u32x4_t v[KB][A];
+    // With one batch per split group (LR == KB: head_dim 64), the next
+    // group's rows are loaded with this group's, so a merge of up to 2 KB
+    // splits takes one round trip and longer ones overlap each batch's loads
+    // with the previous batch's arithmetic.
+    constexpr bool PF = (LR == KB);
+    u32x4_t v[KB][A], v2[PF ? KB : 1][A];
     load_batch(v, r0, r0 + nr);
+    if constexpr (PF) load_batch(v2, r0 + LR, r0 + nr);  // clamped: in bounds when the group is absent
     float wgt[A][C];
 #pragma unroll
     for (int a = 0; a < A; ++a) {
@@ -372,21 +379,23 @@ __device__ __forceinline__ void publish_merge(const RunParams& p, int u, int b, 
       Lt[a] += group_sum<LR>(ls);
       M[a] = Mn;
     }
-#pragma nounroll
-    for (int c = 0; c < C; ++c) {
-      if (c * LR >= nr) break;
-      float wc[A];
+    if constexpr (PF) {
+      // the weights of split group c (a select chain: no indexed array)
+      struct W { float w[A]; };
+      auto group_w = [&](int c) {
+        W x;
 #pragma unroll
-      for (int a = 0; a < A; ++a) {
-        wc[a] = wgt[a][0];
+        for (int a = 0; a < A; ++a) {
+          x.w[a] = wgt[a][0];
 #pragma unroll
-        for (int cc = 1; cc < C; ++cc) wc[a] = (c == cc) ? wgt[a][cc] : wc[a];
-      }
-#pragma unroll
-      for (int q0 = 0; q0 < LR; q0 += KB) {
+          for (int cc = 1; cc < C; ++cc) x.w[a] = (c == cc) ? wgt[a][cc] : x.w[a];
+        }
+        return x;
+      };
+      // rows of the KB splits from c LR + q0 on, held in vv, weighted by wc
+      auto accum = [&](const u32x4_t (&vv)[KB][A], const W wc_, int c, int q0) {
+        const float* wc = wc_.w;
         const int s0 = c * LR + q0;
-        if (s0 >= nr) break;
-        if (s0 > 0) load_batch(v, r0 + s0, r0 + nr);
 #pragma unroll
         for (int q = 0; q < KB; ++q) {
           if (s0 + q >= nr) break;
@@ -395,8 +404,50 @@ __device__ __forceinline__ void publish_merge(const RunParams& p, int u, int b, 
             const float w = mi::lane_shuffle(wc[a], hg * LR + q0 + q);
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-              sum[a][2 * k] += w * mi::bf16_lo(v[q][a][k]);
-              sum[a][2 * k + 1] += w * mi::bf16_hi(v[q][a][k]);
+              sum[a][2 * k] += w * mi::bf16_lo(vv[q][a][k]);
+              sum[a][2 * k + 1] += w * mi::bf16_hi(vv[q][a][k]);
+            }
+          }
+        }
+      };
+      // unrolled: a runtime group index made the compiler turn the weight
+      // select into an indexed stack array
+#pragma unroll
+      for (int c = 0; c < C; c += 2) {
+        if (c * LR >= nr) break;
+        accum(v, group_w(c), c, 0);
+        if ((c + 2) * LR < nr) load_batch(v, r0 + (c + 2) * LR, r0 + nr);
+        if ((c + 1) * LR >= nr) break;
+        accum(v2, group_w(c + 1), c + 1, 0);
+        if ((c + 3) * LR < nr) load_batch(v2, r0 + (c + 3) * LR, r0 + nr);
+      }
+    } else {
+#pragma nounroll
+      for (int c = 0; c < C; ++c) {
+        if (c * LR >= nr) break;
+        float wc[A];
+#pragma unroll
+        for (int a = 0; a < A; ++a) {
+          wc[a] = wgt[a][0];
+#pragma unroll
+          for (int cc = 1; cc < C; ++cc) wc[a] = (c == cc) ? wgt[a][cc] : wc[a];
+        }
+#pragma unroll
+        for (int q0 = 0; q0 < LR; q0 += KB) {
+          const int s0 = c * LR + q0;
+          if (s0 >= nr) break;
+          if (s0 > 0) load_batch(v, r0 + s0, r0 + nr);
+#pragma unroll
+          for (int q = 0; q < KB; ++q) {
+            if (s0 + q >= nr) break;
+#pragma unroll
+            for (int a = 0; a < A; ++a) {
+              const float w = mi::lane_shuffle(wc[a], hg * LR + q0 + q);
+#pragma unroll
+              for (int k = 0; k < 4; ++k) {
+                sum[a][2 * k] += w * mi::bf16_lo(v[q][a][k]);
+                sum[a][2 * k + 1] += w * mi::bf16_hi(v[q][a][k]);
+              }
             }
           }
         }
