@@ -6,9 +6,11 @@
 //
 // One workgroup per token (grid-stride over tokens): the token's slot is a
 // chain of wave-uniform scalar loads (batch index and position, the
-// request's page-list start, the page id) done once per token, then each
+// request's page-list start, the page id) done once per token, and each
 // thread moves 16-byte chunks (8 bf16) of K and the same chunks of V, so a
-// wave writes 1 KiB of contiguous head rows per instruction.
+// wave writes 1 KiB of contiguous head rows per instruction.  The plain
+// append issues its first chunk's loads before the slot chain (18,240
+// prompt rows: 24.2 -> 23.9 us).
 #include <algorithm>
 
 #include "mi_common.h"
@@ -47,15 +49,23 @@ __device__ __forceinline__ uint16_t* token_slot(const int32_t* batch_indices, co
   const const_i32* ps = (const const_i32*)positions;
   const const_i32* ip = (const const_i32*)indptr;
   const const_i32* ix = (const const_i32*)indices;
+  // three round trips: batch index and position together, then the
+  // request's page-list bounds together, then the page id
   const int b = bi[i];
   const int pos = ps[i];
-  if (b < 0 || b >= batch_size || pos < 0) return nullptr;
-  const int64_t it = int64_t(ip[b]) + pos / page_size;
-  if (it >= ip[b + 1]) return nullptr;
+  const bool placed = (b >= 0) & (b < batch_size) & (pos >= 0);
+  const int bc = placed ? b : 0;
+  const int lo = ip[bc], hi = ip[bc + 1];
+  const int64_t it = int64_t(lo) + (placed ? pos : 0) / page_size;
+  if (!placed || it >= hi) return nullptr;
   const int64_t page = ix[it];
   if (page < 0 || page >= num_pages) return nullptr;
   return pool + page * page_stride + int64_t(pos % page_size) * tok_stride;
 }
+
+typedef __attribute__((ext_vector_type(4))) unsigned int ap_u32x4;
+// Buffer resource word 3 for gfx9 raw buffers (32-bit data format, no swizzle).
+constexpr int kBufferWord3 = 0x00020000;
 
 __global__ __launch_bounds__(256) void append_kernel(AppendParams p) {
   const int chunks = p.head_dim >> 3;
@@ -63,17 +73,36 @@ __global__ __launch_bounds__(256) void append_kernel(AppendParams p) {
   const int64_t tok_stride = int64_t(p.num_kv_heads) * p.head_dim;
   const int64_t kv_stride = int64_t(p.page_size) * tok_stride;
   const int64_t page_stride = 2 * kv_stride;
+  const int u0 = threadIdx.x;
+  const int h0 = u0 / chunks, c0 = (u0 - h0 * chunks) * 8;
   for (int64_t i = blockIdx.x; i < p.num_tokens; i += gridDim.x) {
+    // the first chunk's rows do not depend on the slot: their loads go out
+    // before the slot's chain of scalar loads
+    uint4 k0 = make_uint4(0, 0, 0, 0), v0 = make_uint4(0, 0, 0, 0);
+    if (u0 < per_token) {
+      k0 = mi::load16(p.key + i * p.ks_tok + h0 * p.ks_head + c0);
+      v0 = mi::load16(p.value + i * p.vs_tok + h0 * p.vs_head + c0);
+    }
     uint16_t* slot = token_slot(p.batch_indices, p.positions, p.indptr, p.indices, i, p.batch_size, p.num_pages,
                                 p.page_size, p.pool, page_stride, tok_stride);
-    if (!slot) continue;
-    for (int u = threadIdx.x; u < per_token; u += blockDim.x) {
+    // stores through a descriptor of the slot's row (size 0 when the token is
+    // not placed: the stores write nothing), so the loads above are used on
+    // every path and stay ahead of the chain
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        slot ? (void*)slot : (void*)p.pool, (short)0, slot ? int(kv_stride * 2 + tok_stride * 2) : 0, kBufferWord3);
+    if (u0 < per_token) {
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(ap_u32x4, k0), rs, (h0 * p.head_dim + c0) * 2, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(ap_u32x4, v0), rs,
+                                             int(kv_stride * 2) + (h0 * p.head_dim + c0) * 2, 0, 0);
+    }
+    for (int u = u0 + int(blockDim.x); u < per_token; u += blockDim.x) {
       const int h = u / chunks;
       const int c = (u - h * chunks) * 8;
       const uint4 kv = mi::load16(p.key + i * p.ks_tok + h * p.ks_head + c);
       const uint4 vv = mi::load16(p.value + i * p.vs_tok + h * p.vs_head + c);
-      mi::store16(slot + h * p.head_dim + c, kv);
-      mi::store16(slot + kv_stride + h * p.head_dim + c, vv);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(ap_u32x4, kv), rs, (h * p.head_dim + c) * 2, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(ap_u32x4, vv), rs,
+                                             int(kv_stride * 2) + (h * p.head_dim + c) * 2, 0, 0);
     }
   }
 }
