@@ -89,6 +89,28 @@ def test_out_of_range_rows_not_written(dev):
     assert changed == [int(indices[1])]  # only page holding position 19
 
 
+@pytest.mark.parametrize("hkv,d", [(2, 64), (8, 128)])
+def test_unplaced_rows_among_placed_ones(dev, hkv, d):
+    """A negative batch index, one past the batch, a negative position and a
+    page id outside the pool write nothing, while the rows around them land;
+    the K / V loads of every row are issued before its slot is known."""
+    lens = [20, 40]
+    g, pool, indptr, indices, last = _setup(lens, hkv, d, 16, seed=4)
+    indices = indices.clone()
+    indices[indptr[1] + 2] = pool.shape[0] + 5  # request 1's positions 32..39: a page outside the pool
+    bi = [0, -1, 2, 1, 1, 1, 0]
+    pos = [5, 3, 0, -3, 20, 35, 19]
+    k = torch.randn(len(bi), hkv, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(len(bi), hkv, d, generator=g).to(torch.bfloat16)
+    got = _run(dev, pool, k, v, bi, pos, indices, indptr, last)
+    ok = [i for i in range(len(bi)) if 0 <= bi[i] < len(lens) and pos[i] >= 0]
+    want = opg.append(pool, k[ok], v[ok], [bi[i] for i in ok], [pos[i] for i in ok], indices.tolist(), indptr)
+    assert torch.equal(got, want)
+    changed = set((got != pool).flatten(1).any(dim=1).nonzero().flatten().tolist())
+    # request 0's positions 5 and 19 (its pages 0 and 1), request 1's position 20 (its page 1)
+    assert changed == {int(indices[0]), int(indices[1]), int(indices[indptr[1] + 1])}
+
+
 def test_empty_append_is_noop(dev):
     from minimal_inference_amd.page import append_paged_kv_cache
 
