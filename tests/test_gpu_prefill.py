@@ -67,6 +67,19 @@ def test_kv_longer_than_q_bottom_right_causal(dev, parity, hq, hkv, d):
     parity(out, ref)
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64)])
+def test_zero_length_query_spans_in_a_ragged_batch(dev, parity, hq, hkv, d):
+    """Requests with no query rows -- one with cached tokens, one empty --
+    between requests with rows (one of them chunked: 10 rows over 64 tokens)
+    get no tiles, and the rows around them are unaffected."""
+    kv_lens = [37, 200, 0, 64, 1]
+    qo_lens = [37, 0, 0, 10, 1]
+    b = make_paged_batch(kv_lens, hq, hkv, d, seed=41)
+    out, ref = _run(dev, b, qo_lens, hq, hkv, d, seed=41)
+    assert out.shape[0] == sum(qo_lens)
+    parity(out, ref)
+
+
 def test_non_causal(dev, parity):
     lens = [50, 129]
     b = make_paged_batch(lens, 16, 4, 64, seed=6)
