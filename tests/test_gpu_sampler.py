@@ -80,7 +80,10 @@ def _chi2_ok(counts: np.ndarray, probs: np.ndarray, n: int) -> bool:
     return chi2.sf(stat, max(dof, 1)) > 1e-4
 
 
-@pytest.mark.parametrize("temp,top_p", [(1.0, None), (0.7, None), (0.7, 0.9), (1.3, 0.5)])
+@pytest.mark.parametrize("temp,top_p", [(1.0, None), (0.7, None), (0.7, 0.9), (1.3, 0.5),
+                                        # extremes: a near-greedy temperature, a nucleus of the top
+                                        # token alone, a flat high-temperature nucleus
+                                        (0.2, None), (1.0, 0.001), (2.5, 0.95)])
 def test_distribution_matches_oracle(dev, temp, top_p):
     V, rows, calls = 64, 2048, 8
     g = torch.Generator().manual_seed(int(temp * 10) + (0 if top_p is None else 7))
