@@ -94,6 +94,21 @@ def test_head_dim_64_lane_groups(dev, parity, lens):
     parity(_decode(dev, b, 14, 2, 64), _ref(b))
 
 
+@pytest.mark.parametrize("sm_scale", [0.3, 0.02])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64)])
+def test_explicit_softmax_scale(dev, parity, sm_scale, hq, hkv, d):
+    """plan(sm_scale=...) replaces 1/sqrt(head_dim): a sharper (0.3) and a
+    flatter (0.02) softmax against the oracle at the same scale."""
+    lens = [1, 40, 300, 2000]
+    b = make_paged_batch(lens, hq, hkv, d, seed=57)
+    pool, q, ip, ix, lp = to_dev(b, dev)
+    w = _wrapper(dev)
+    w.plan(ip, ix, lp, hq, hkv, d, 16, sm_scale=sm_scale)
+    out = w.run(q, pool).float().cpu()
+    ref = oatt.decode(b["q"], b["pool"], b["indptr"], b["indices"].tolist(), b["last"], sm_scale=sm_scale)
+    parity(out, ref)
+
+
 def test_empty_request_gives_zero(dev, parity):
     b = make_paged_batch([0, 40], 8, 2, 64, seed=5)
     out = _decode(dev, b, 8, 2, 64)

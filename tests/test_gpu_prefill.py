@@ -80,6 +80,29 @@ def test_zero_length_query_spans_in_a_ragged_batch(dev, parity, hq, hkv, d):
     parity(out, ref)
 
 
+@pytest.mark.parametrize("sm_scale", [0.3, 0.02])
+def test_explicit_softmax_scale(dev, parity, sm_scale):
+    """plan(sm_scale=...) replaces 1/sqrt(head_dim) in the causal prefill."""
+    from minimal_inference_amd.prefill import BatchPrefillWithPagedKVCacheWrapper
+
+    hq, hkv, d = 32, 8, 128
+    lens = [37, 300, 5]
+    b = make_paged_batch(lens, hq, hkv, d, seed=58)
+    g = torch.Generator().manual_seed(58)
+    q = torch.randn(sum(lens), hq, d, generator=g).to(torch.bfloat16)
+    qo = [0]
+    for x in lens:
+        qo.append(qo[-1] + x)
+    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(64 << 20, dtype=torch.uint8, device=dev), "NHD")
+    w.plan(torch.tensor(qo, dtype=torch.int32, device=dev), torch.tensor(b["indptr"], dtype=torch.int32, device=dev),
+           b["indices"].to(dev), torch.tensor(b["last"], dtype=torch.int32, device=dev), hq, hkv, d, 16,
+           causal=True, sm_scale=sm_scale)
+    out = w.run(q.to(dev), b["pool"].to(dev)).float().cpu()
+    ref = oatt.prefill(q, b["pool"], qo, b["indptr"], b["indices"].tolist(), b["last"], causal=True,
+                       sm_scale=sm_scale)
+    parity(out, ref)
+
+
 def test_non_causal(dev, parity):
     lens = [50, 129]
     b = make_paged_batch(lens, 16, 4, 64, seed=6)
