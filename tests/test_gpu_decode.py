@@ -109,6 +109,23 @@ def test_explicit_softmax_scale(dev, parity, sm_scale, hq, hkv, d):
     parity(out, ref)
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64)])
+def test_large_scores_lazy_rescale(dev, parity, hq, hkv, d):
+    """q and K scaled by 6: scores spread over tens of natural
+    units, so the running max grows past the lazy-rescale margin (2^8 in the
+    exp2 domain) many times within a unit and across splits."""
+    lens = [5, 300, 2000, 4100]
+    b = make_paged_batch(lens, hq, hkv, d, seed=61)
+    b["pool"][:, 0] = (b["pool"][:, 0].float() * 6).to(torch.bfloat16)
+    # V / 4 keeps the near one-hot outputs (single V entries) near unit size,
+    # where the max-abs bound applies
+    b["pool"][:, 1] = (b["pool"][:, 1].float() / 4).to(torch.bfloat16)
+    b["q"] = (b["q"].float() * 6).to(torch.bfloat16)
+    out = _decode(dev, b, hq, hkv, d)
+    assert torch.isfinite(out).all()
+    parity(out, _ref(b))
+
+
 def test_empty_request_gives_zero(dev, parity):
     b = make_paged_batch([0, 40], 8, 2, 64, seed=5)
     out = _decode(dev, b, 8, 2, 64)

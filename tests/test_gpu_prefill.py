@@ -103,6 +103,32 @@ def test_explicit_softmax_scale(dev, parity, sm_scale):
     parity(out, ref)
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64)])
+def test_large_scores_lazy_rescale(dev, parity, hq, hkv, d):
+    """q and K scaled by 6: the row maxima grow past the lazy
+    rescale margin many times along a row's key tiles."""
+    lens = [300, 777]
+    b = make_paged_batch(lens, hq, hkv, d, seed=62)
+    b["pool"][:, 0] = (b["pool"][:, 0].float() * 6).to(torch.bfloat16)
+    # V / 4 keeps the near one-hot outputs (single V entries) near unit size,
+    # where the max-abs bound applies
+    b["pool"][:, 1] = (b["pool"][:, 1].float() / 4).to(torch.bfloat16)
+    from minimal_inference_amd.prefill import BatchPrefillWithPagedKVCacheWrapper
+
+    g = torch.Generator().manual_seed(62)
+    q = (torch.randn(sum(lens), hq, d, generator=g) * 6).to(torch.bfloat16)
+    qo = [0]
+    for x in lens:
+        qo.append(qo[-1] + x)
+    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(64 << 20, dtype=torch.uint8, device=dev), "NHD")
+    w.plan(torch.tensor(qo, dtype=torch.int32, device=dev), torch.tensor(b["indptr"], dtype=torch.int32, device=dev),
+           b["indices"].to(dev), torch.tensor(b["last"], dtype=torch.int32, device=dev), hq, hkv, d, 16, causal=True)
+    out = w.run(q.to(dev), b["pool"].to(dev)).float().cpu()
+    assert torch.isfinite(out).all()
+    ref = oatt.prefill(q, b["pool"], qo, b["indptr"], b["indices"].tolist(), b["last"], causal=True)
+    parity(out, ref)
+
+
 def test_non_causal(dev, parity):
     lens = [50, 129]
     b = make_paged_batch(lens, 16, 4, 64, seed=6)
