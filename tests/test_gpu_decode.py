@@ -126,6 +126,22 @@ def test_large_scores_lazy_rescale(dev, parity, hq, hkv, d):
     parity(out, _ref(b))
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 2, 64)])
+def test_one_long_request_among_short_ones(dev, parity, hq, hkv, d):
+    """A 32,768-token request among forty 16-token ones: the plan's uniform
+    item length gives the long request well over 64 splits, so its last
+    arriver merges them in several rounds of 64."""
+    lens = [32768] + [16] * 40
+    b = make_paged_batch(lens, hq, hkv, d, seed=63)
+    w = _wrapper(dev)
+    out = _decode(dev, b, hq, hkv, d, w=w)
+    # the plan's first work item (128 bytes after a 256-byte header) is split 0
+    # of the long request; word 29 of an item is its split count
+    nsplit = int(w._ws[256:384].view(torch.int32)[29])
+    assert nsplit > 64
+    parity(out, _ref(b))
+
+
 def test_empty_request_gives_zero(dev, parity):
     b = make_paged_batch([0, 40], 8, 2, 64, seed=5)
     out = _decode(dev, b, 8, 2, 64)
