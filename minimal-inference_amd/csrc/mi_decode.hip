@@ -1092,6 +1092,11 @@ int launch_run(const char* who, bool rope, RunParams rp, void* workspace, size_t
   const DecodeLayout L = decode_layout(batch_size, num_qo_heads, num_kv_heads, head_dim, max_units);
   if (!workspace || workspace_bytes < L.total)
     return mi::fail(MI_ERR_WORKSPACE, "%s: workspace %zu bytes, need %zu", who, workspace_bytes, L.total);
+  // the plan's own bound (every wave reads a work item before it knows the
+  // unit count, clamped to the item array, which must not be empty)
+  if (L.max_items < batch_size)
+    return mi::fail(MI_ERR_WORKSPACE, "%s: room for %d units, need at least batch*kv_heads = %d", who, max_units,
+                    batch_size * num_kv_heads);
   if (!rp.q || !rp.pool || !rp.indices || !rp.out) return mi::fail(MI_ERR_INVALID, "%s: null pointer argument", who);
   if ((reinterpret_cast<uintptr_t>(rp.q) & 15) || (reinterpret_cast<uintptr_t>(rp.pool) & 15) || rp.q_sb % 8 ||
       rp.q_sh % 8)

@@ -56,3 +56,12 @@ def test_host_only_calls_and_error_reporting():
     assert rc == _lib.MI_ERR_UNSUPPORTED
     rc = lib.mi_decode_plan(None, 0, None, None, None, 1, 32, 8, 128, 16, 0, None)
     assert rc == _lib.MI_ERR_WORKSPACE
+    # a run whose work list could not hold one item per request (max_units 4
+    # for 8 KV heads) is refused before any launch, like the plan
+    import ctypes
+
+    ws = ctypes.create_string_buffer(1 << 20)
+    rc = lib.mi_decode_run(ctypes.addressof(ws), 1 << 20, None, 0, 0, None, 0, None, None, 0, 0,
+                           2, 32, 8, 128, 16, 0.0, 4, None)
+    assert rc == _lib.MI_ERR_WORKSPACE
+    assert "room for 4 units" in _lib.last_error()
