@@ -304,7 +304,7 @@ __device__ __forceinline__ void publish_merge(const RunParams& p, int u, int b, 
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   int prev = 0;
-  int* counter = p.counters + b * p.hkv + hkv;
+  int* counter = p.counters + (b * p.hkv + hkv) * kCounterStride;
   if (lane == 0) prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   prev = mi::read_lane_i(prev, 0);
   if (prev != nsplit - 1) return;

@@ -31,6 +31,10 @@ constexpr int kUnitsPerCU = MI_DECODE_UNITS_PER_CU;
 #define MI_DECODE_MERGE_BUDGET 40  // average splits x group per (request, KV head) the plan aims under
 #endif
 constexpr int kInlinePages = 24;
+// Ints between two per-(request, KV head) merge counters: one 128-byte line
+// each, so the units' counting atomics on different counters do not queue on
+// one line.
+constexpr int kCounterStride = 32;
 constexpr int kPlanThreads = 1024;  // both planning kernels run one workgroup of this size
 
 // One item = a contiguous page range of one request.  Read by a wave with one
@@ -74,7 +78,7 @@ inline DecodeLayout decode_layout(int batch, int hq, int hkv, int head_dim, int 
   L.items = off;
   off = align_up(off + size_t(L.max_items) * sizeof(DecodeItem), 256);
   L.counters = off;
-  off = align_up(off + size_t(batch) * hkv * sizeof(int), 256);
+  off = align_up(off + size_t(batch) * hkv * kCounterStride * sizeof(int), 256);
   L.pml = off;
   off = align_up(off + size_t(max_units) * group * 2 * sizeof(float), 256);
   L.po = off;
@@ -87,7 +91,7 @@ inline DecodeLayout decode_layout(int batch, int hq, int hkv, int head_dim, int 
 // it, capped at 65536 (enough for 8-page items over ~32M tokens x heads).
 inline int units_that_fit(size_t bytes, int batch, int hq, int hkv, int head_dim) {
   const int group = hq / hkv;
-  const size_t fixed = 256 + 2 * 256 + size_t(batch) * hkv * sizeof(int);
+  const size_t fixed = 256 + 2 * 256 + size_t(batch) * hkv * kCounterStride * sizeof(int);
   if (bytes <= fixed) return 0;
   const size_t per_unit = sizeof(DecodeItem) / size_t(hkv) + 1 + size_t(group) * (2 * sizeof(float) + head_dim * sizeof(uint16_t));
   size_t n = (bytes - fixed) / per_unit;
@@ -325,7 +329,7 @@ __device__ inline void plan_items(const PlanParams& p, int q16, bool cached, int
     running += chunk_total;
     __syncthreads();  // the next round rewrites scan and s_*
   }
-  for (int i = t; i < p.batch * p.hkv; i += blockDim.x) p.counters[i] = 0;
+  for (int i = t; i < p.batch * p.hkv; i += blockDim.x) p.counters[i * kCounterStride] = 0;
   if (t == 0) write_header(p, running, q16);
 }
 
@@ -357,7 +361,7 @@ __device__ inline void plan_small(const PlanParams& p, const int* s_np, const in
   __syncthreads();
   const int total = scan[63];
   for (int idx = t; idx < total; idx += blockDim.x) write_item(p, idx, scan, 64, 0, 0, s_np, s_pb0, s_lpl);
-  for (int i = t; i < p.batch * p.hkv; i += blockDim.x) p.counters[i] = 0;
+  for (int i = t; i < p.batch * p.hkv; i += blockDim.x) p.counters[i * kCounterStride] = 0;
   if (t == 0) write_header(p, total, s_q16);
 }
 
