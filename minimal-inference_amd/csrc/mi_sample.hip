@@ -77,6 +77,8 @@ __device__ __forceinline__ float u01(uint32_t x) { return (float(x >> 8) + 0.5f)
 constexpr int kT = 256;              // threads per workgroup
 constexpr int kGroupsPerThread = 4;  // 4-token groups per thread
 constexpr int kChunk = kT * kGroupsPerThread * 4;  // 4,096 tokens per workgroup
+// ints between two rows' counters in the workspace (one 128-byte line each)
+constexpr int kCntStride = 32;
 constexpr int kBins = 1024;          // histogram bins: key >> 6
 constexpr int kSub = 64;             // keys per bin
 constexpr int kSup = 32;             // super-bins of kBins / kSup bins
@@ -616,7 +618,7 @@ __global__ __launch_bounds__(kT) void sample_pass2(SampleParams p) {
       coherent_store(&p.sub_mass[size_t(pc) * kSub + tid], sub_mass[tid]);
       coherent_store(&p.sub_best[size_t(pc) * kSub + tid], sub_best[tid]);
     }
-    if (last_of_row(&p.cnt[row], C, &s_flag)) {
+    if (last_of_row(&p.cnt[row * kCntStride], C, &s_flag)) {
       unsigned long long bb = 0;
       for (int cc = tid; cc < C; cc += kT) bb = max(bb, coherent_load(&p.best[base + cc]));
       if (ri.bstar >= 0) {
@@ -686,8 +688,10 @@ SampleLayout sample_layout(int batch, int vocab) {
   };
   // counters at fixed offsets, sized for the largest batch a call takes, so
   // calls of different batch sizes on one workspace never lay partials over
-  // them (every call leaves them at zero)
-  L.cnt = take(size_t(kMaxRows) * sizeof(int));
+  // them (every call leaves them at zero); one 128-byte line per row, so the
+  // rows' workgroups do not queue their counting atomics on a shared line
+  // (B=32 x 32,768: 19.1 -> 18.2 us; 48 x 152,064 top-p: 40.5 -> 35.7 us)
+  L.cnt = take(size_t(kMaxRows) * kCntStride * sizeof(int));
   L.off_copy = take(sizeof(uint64_t));
   L.part = take(rc * kNW * sizeof(unsigned long long));
   L.cmax = take(rc * sizeof(uint32_t));
