@@ -65,3 +65,10 @@ def test_host_only_calls_and_error_reporting():
                            2, 32, 8, 128, 16, 0.0, 4, None)
     assert rc == _lib.MI_ERR_WORKSPACE
     assert "room for 4 units" in _lib.last_error()
+    # the sampler takes at most 65,535 rows (one workgroup row each in the
+    # launch grid's y dimension, one counter line each in the workspace)
+    assert lib.mi_sample_workspace_size(65535, 32768) > lib.mi_sample_workspace_size(1, 32768) > 0
+    assert lib.mi_sample_workspace_size(65536, 32768) == 0
+    rc = lib.mi_sample(None, 32768, 65536, 32768, None, None, 0, None, None, None, 0, None)
+    assert rc == _lib.MI_ERR_INVALID
+    assert "over 65535 rows" in _lib.last_error()

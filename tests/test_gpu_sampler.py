@@ -273,6 +273,32 @@ def test_largest_vocabulary_and_one_past_it(dev):
         s.sample(torch.zeros(rows, V + 1, dtype=torch.bfloat16, device=dev))
 
 
+def test_largest_batch_twice(dev):
+    """65,535 rows (the most one call takes; the last row's counter is the
+    workspace's last), twice in a row on one workspace: greedy ids bit-exact,
+    draws inside the nucleus; the second call starts from the counters the
+    first left at zero."""
+    rows, V = 65535, 200
+    g = torch.Generator().manual_seed(35)
+    s = _sampler(dev, rows, seed=5)
+    temps = [0.0 if i % 3 == 0 else 0.8 for i in range(rows)]
+    tops = [0.9 if i % 2 == 0 else 1.0 for i in range(rows)]
+    s.set_params(temps, tops)
+    greedy = torch.tensor([t == 0.0 for t in temps])
+    sampled = ~greedy
+    for call in range(2):
+        logits = (torch.randn(rows, V, generator=g) * 2).to(torch.bfloat16)
+        got = s.sample(logits.to(dev)).cpu()
+        assert torch.equal(got[greedy], osmp.greedy(logits[greedy])), call
+        # the oracle's nucleus is a per-row loop: every 97th sampled row and
+        # the last rows (the highest counters) are checked
+        idx = sampled.nonzero().flatten()
+        idx = torch.cat([idx[::97], idx[-24:]])
+        probs = osmp.distribution(logits[idx], [temps[i] for i in idx.tolist()], [tops[i] for i in idx.tolist()])
+        kept = probs.gather(1, got[idx].view(-1, 1).long()).flatten()
+        assert bool((kept > 0).all()), call
+
+
 def test_reference_sample_semantics_on_the_gpu(dev):
     """The oracle's restatement of sample() (scheduler.py:310-316) against
     torch's own GPU kernels: a bf16 tensor divided by a Python float (the
