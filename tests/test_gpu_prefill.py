@@ -129,10 +129,22 @@ def test_large_scores_lazy_rescale(dev, parity, hq, hkv, d):
     parity(out, ref)
 
 
-def test_non_causal(dev, parity):
-    lens = [50, 129]
-    b = make_paged_batch(lens, 16, 4, 64, seed=6)
-    out, ref = _run(dev, b, lens, 16, 4, 64, causal=False, seed=6)
+@pytest.mark.parametrize("hq,hkv,d", [(16, 4, 64), (32, 8, 128), (28, 4, 128), (16, 4, 256)])
+def test_non_causal(dev, parity, hq, hkv, d):
+    lens = [50, 129, 1, 300]
+    b = make_paged_batch(lens, hq, hkv, d, seed=6)
+    out, ref = _run(dev, b, lens, hq, hkv, d, causal=False, seed=6)
+    parity(out, ref)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64)])
+def test_non_causal_kv_longer_than_q(dev, parity, hq, hkv, d):
+    """Non-causal rows over a longer cached context: every row sees every
+    key, including the keys past its own position."""
+    kv_lens = [100, 260, 33]
+    qo_lens = [20, 64, 1]
+    b = make_paged_batch(kv_lens, hq, hkv, d, seed=44)
+    out, ref = _run(dev, b, qo_lens, hq, hkv, d, causal=False, seed=44)
     parity(out, ref)
 
 
