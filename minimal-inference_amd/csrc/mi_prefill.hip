@@ -193,11 +193,12 @@ struct RunParams {
   const PrefillTile* tiles;
   const uint16_t* q;
   int64_t q_st, q_sh;
+  int64_t q_ext;  // elements one position's heads span: (heads - 1) * q_sh + head_dim
   const uint16_t* pool;
   int64_t num_pages;
   const int32_t* indices;
   uint16_t* out;
-  int64_t o_st, o_sh;
+  int64_t o_st, o_sh, o_ext;
   int64_t total_q;
   int hkv, group, causal, bm;
   float scale_log2;
@@ -316,7 +317,8 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
   int lpos[T::MAXRB];     // this lane's row's position within the tile (-1: none)
   int nblk = 0;
   const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(p.q + int64_t(t.q_begin) * p.q_st), (short)0, int(int64_t(t.q_rows) * p.q_st * 2), kBufferWord3);
+      (void*)(p.q + int64_t(t.q_begin) * p.q_st), (short)0,
+      int((int64_t(max(t.q_rows, 1) - 1) * p.q_st + p.q_ext) * 2), kBufferWord3);
 #pragma unroll
   for (int r = 0; r < T::MAXRB; ++r) {
     const int rb = w + T::WAVES * r;
@@ -678,7 +680,8 @@ __global__ __launch_bounds__(64 * waves_for(D)) __attribute__((amdgpu_waves_per_
   }
   __syncthreads();
   const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(p.out + int64_t(t.q_begin) * p.o_st), (short)0, int(int64_t(t.q_rows) * p.o_st * 2), kBufferWord3);
+      (void*)(p.out + int64_t(t.q_begin) * p.o_st), (short)0,
+      int((int64_t(max(t.q_rows, 1) - 1) * p.o_st + p.o_ext) * 2), kBufferWord3);
   // lane (g, n) reads columns 32q + 8g + [0, 8) of row n
   const int rcol = g * kOutBlk + (n >> 2) * 32 + (n & 3) * 8;
 #pragma unroll
@@ -756,8 +759,11 @@ extern "C" int mi_prefill_run(void* workspace, size_t workspace_bytes, const voi
   if (total_q == 0 || batch_size == 0) return MI_OK;
   if (!q || !paged_kv_cache || !kv_indices || !out) return mi::fail(MI_ERR_INVALID, "prefill run: null pointer");
   if ((reinterpret_cast<uintptr_t>(q) & 15) || (reinterpret_cast<uintptr_t>(paged_kv_cache) & 15) ||
-      q_stride_token % 8 || q_stride_head % 8)
-    return mi::fail(MI_ERR_INVALID, "prefill run: q rows and pool must be 16-byte aligned");
+      (reinterpret_cast<uintptr_t>(out) & 15) || q_stride_token % 8 || q_stride_head % 8 ||
+      out_stride_token % 8 || out_stride_head % 8)
+    return mi::fail(MI_ERR_INVALID, "prefill run: q rows, out rows and pool must be 16-byte aligned");
+  if (q_stride_token < 0 || q_stride_head < 0 || out_stride_token < 0 || out_stride_head < 0)
+    return mi::fail(MI_ERR_INVALID, "prefill run: negative stride");
   const int64_t grid = int64_t(tile_capacity(batch_size, total_q)) * num_kv_heads;
   if (grid > 0x7fffffff) return mi::fail(MI_ERR_INVALID, "prefill run: too many tiles");
   char* ws = static_cast<char*>(workspace);
@@ -778,6 +784,16 @@ extern "C" int mi_prefill_run(void* workspace, size_t workspace_bytes, const voi
   rp.group = num_qo_heads / num_kv_heads;
   rp.causal = causal ? 1 : 0;
   rp.bm = rows_per_tile(rp.group, head_dim);
+  // a tile addresses its q / out rows through one buffer descriptor each, by
+  // 32-bit byte offsets from its first position: any strides (heads inside a
+  // position's row, or head-major) whose tile extent fits
+  rp.q_ext = int64_t(num_qo_heads - 1) * q_stride_head + head_dim;
+  rp.o_ext = int64_t(num_qo_heads - 1) * out_stride_head + head_dim;
+  const int64_t q_span = (int64_t(rp.bm) - 1) * q_stride_token + rp.q_ext;
+  const int64_t o_span = (int64_t(rp.bm) - 1) * out_stride_token + rp.o_ext;
+  if (q_span > 0x3fffffff || o_span > 0x3fffffff)
+    return mi::fail(MI_ERR_INVALID, "prefill run: q / out strides span %lld / %lld elements per tile (at most 2^30)",
+                    (long long)q_span, (long long)o_span);
   const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf(float(head_dim));
   rp.scale_log2 = scale * mi::kLog2e;
   const dim3 g{static_cast<uint32_t>(grid), 1u, 1u};

@@ -72,3 +72,20 @@ def test_host_only_calls_and_error_reporting():
     rc = lib.mi_sample(None, 32768, 65536, 32768, None, None, 0, None, None, None, 0, None)
     assert rc == _lib.MI_ERR_INVALID
     assert "over 65535 rows" in _lib.last_error()
+    # prefill run: out rows must be 16-byte aligned, and a tile's q / out rows
+    # must span at most 2^30 elements (its 32-bit buffer offsets); both refused
+    # before any launch (the pointers are never dereferenced)
+    need = lib.mi_prefill_workspace_size(1, 64)
+    pws = ctypes.create_string_buffer(need)
+    fake = 1 << 20
+    args = dict(q_st=32 * 128, q_sh=128, out=fake, o_st=32 * 128, o_sh=128)
+
+    def prefill_rc(**kw):
+        a = {**args, **kw}
+        return lib.mi_prefill_run(ctypes.addressof(pws), need, fake, a["q_st"], a["q_sh"], fake, 16, fake, a["out"],
+                                  a["o_st"], a["o_sh"], 1, 64, 32, 8, 128, 16, 1, 0.0, None)
+
+    assert prefill_rc(out=fake + 8) == _lib.MI_ERR_INVALID
+    assert "16-byte aligned" in _lib.last_error()
+    assert prefill_rc(q_sh=1 << 26) == _lib.MI_ERR_INVALID
+    assert "2^30" in _lib.last_error()

@@ -129,6 +129,35 @@ def test_large_scores_lazy_rescale(dev, parity, hq, hkv, d):
     parity(out, ref)
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64), (16, 4, 256)])
+def test_head_major_q_and_out_views(dev, parity, hq, hkv, d):
+    """q and out as head-major views ([heads, rows, head_dim] storage seen as
+    [rows, heads, head_dim]: a head stride of rows * head_dim, larger than
+    the row stride), as a single prompt's q.permute(0, 2, 1, 3).reshape(...)
+    is; every tile's rows and heads are read and written through them."""
+    from minimal_inference_amd.prefill import BatchPrefillWithPagedKVCacheWrapper
+
+    lens = [37, 300, 5, 129]
+    b = make_paged_batch(lens, hq, hkv, d, seed=47)
+    g = torch.Generator().manual_seed(47)
+    q = torch.randn(sum(lens), hq, d, generator=g).to(torch.bfloat16)
+    qo = [0]
+    for x in lens:
+        qo.append(qo[-1] + x)
+    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(64 << 20, dtype=torch.uint8, device=dev), "NHD")
+    w.plan(torch.tensor(qo, dtype=torch.int32, device=dev), torch.tensor(b["indptr"], dtype=torch.int32, device=dev),
+           b["indices"].to(dev), torch.tensor(b["last"], dtype=torch.int32, device=dev), hq, hkv, d, 16, causal=True)
+    q_hm = q.transpose(0, 1).contiguous().to(dev).transpose(0, 1)
+    out_hm = torch.full((hq, sum(lens), d), float("nan"), dtype=torch.bfloat16, device=dev).transpose(0, 1)
+    assert q_hm.stride() == (d, sum(lens) * d, 1) and out_hm.stride() == q_hm.stride()
+    got = w.run(q_hm, b["pool"].to(dev), out=out_hm)
+    assert got.data_ptr() == out_hm.data_ptr()
+    ref = oatt.prefill(q, b["pool"], qo, b["indptr"], b["indices"].tolist(), b["last"], causal=True)
+    out = out_hm.float().cpu()
+    assert torch.isfinite(out).all()
+    parity(out, ref)
+
+
 @pytest.mark.parametrize("hq,hkv,d", [(16, 4, 64), (32, 8, 128), (28, 4, 128), (16, 4, 256)])
 def test_non_causal(dev, parity, hq, hkv, d):
     lens = [50, 129, 1, 300]
