@@ -163,3 +163,87 @@ def test_decode_step_in_the_reference_call_form(dev, parity, hq, hkv, d):
     ref = oatt.decode(q[:, :, 0], want_pool, b["indptr"], b["indices"].tolist(), b["last"])
     assert out.shape == (B, hq, d)
     parity(out.float().cpu(), ref)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (32, 8, 128)])
+def test_decode_graph_runner_in_the_reference_call_form(dev, parity, hq, hkv, d):
+    """The reference's graph runner (scheduler.py:353-469, 900-916): static
+    buffers initialised as at scheduler.py:366-374 (indptr zeros, indices all
+    the scratch page, last_page_len ones, batch_indices arange, positions
+    zeros); a plan on that dummy metadata with indices sliced to the batch
+    size (scheduler.py:402-413); three warm-up passes of append + run on a
+    side stream and one captured pass; then, per step, the real metadata
+    copied into the static buffers, a plan on slices of them outside the
+    graph, and a replay. Pools bit-exact and outputs within the parity bar
+    at every replay."""
+    from minimal_inference_amd.decode import BatchDecodeWithPagedKVCacheWrapper
+    from minimal_inference_amd.page import append_paged_kv_cache
+
+    B, num_pages, max_num_pages = 8, 400, 512
+    scratch_page = num_pages - 1
+    group = hq // hkv
+    padded = hkv * _padded_group(group)
+    kv_page_indptr = torch.zeros(B + 1, dtype=torch.int32, device=dev)
+    kv_page_indices = torch.full((max_num_pages,), scratch_page, dtype=torch.int32, device=dev)
+    kv_last_page_len = torch.ones(B, dtype=torch.int32, device=dev)
+    batch_indices = torch.arange(B, dtype=torch.int32, device=dev)
+    positions = torch.zeros(B, dtype=torch.int32, device=dev)
+    q_in = torch.zeros(B, hq, 1, d, dtype=torch.bfloat16, device=dev)
+    k_in = torch.zeros(B, hkv, 1, d, dtype=torch.bfloat16, device=dev)
+    v_in = torch.zeros(B, hkv, 1, d, dtype=torch.bfloat16, device=dev)
+    kv_data = torch.zeros(num_pages, 2, 16, hkv, d, dtype=torch.bfloat16, device=dev)
+
+    wrapper = BatchDecodeWithPagedKVCacheWrapper(torch.empty(128 << 20, dtype=torch.uint8, device=dev),
+                                                 kv_layout="NHD")
+    plan_kw = dict(num_qo_heads=padded, num_kv_heads=hkv, head_dim=d, page_size=16, pos_encoding_mode="NONE",
+                   q_data_type=torch.bfloat16, data_type=torch.bfloat16)
+    wrapper.plan(indptr=kv_page_indptr, indices=kv_page_indices[:B], last_page_len=kv_last_page_len, **plan_kw)
+
+    def layer():
+        k_append = k_in.permute(0, 2, 1, 3).reshape(-1, hkv, d)
+        v_append = v_in.permute(0, 2, 1, 3).reshape(-1, hkv, d)
+        append_paged_kv_cache(k_append, v_append, batch_indices, positions, kv_data, kv_page_indices,
+                              kv_page_indptr, kv_last_page_len)
+        q_fi = q_in.squeeze(2)
+        if padded != hq:
+            q_fi = _pad_heads(q_fi, hkv, group)
+        out = wrapper.run(q_fi, kv_data)
+        return _strip_heads(out, hkv, group) if padded != hq else out
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            layer()
+    s.synchronize()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = layer()
+
+    g = torch.Generator().manual_seed(d + hq)
+    for step, lens in enumerate([[40, 1, 300, 17, 64, 129, 5, 16], [41, 2, 301, 18, 65, 130, 6, 17],
+                                 [900, 33, 2, 1, 1000, 16, 17, 250]]):
+        b = make_paged_batch(lens, hq, hkv, d, num_pages=num_pages - 1, seed=step + 70)
+        pool = torch.cat([b["pool"], torch.zeros(1, 2, 16, hkv, d, dtype=torch.bfloat16)])
+        kv_data.copy_(pool)
+        q = torch.randn(B, hq, 1, d, generator=g).to(torch.bfloat16)
+        k = torch.randn(B, hkv, 1, d, generator=g).to(torch.bfloat16)
+        v = torch.randn(B, hkv, 1, d, generator=g).to(torch.bfloat16)
+        q_in.copy_(q)
+        k_in.copy_(k)
+        v_in.copy_(v)
+        n_idx = b["indices"].numel()
+        kv_page_indptr.copy_(torch.tensor(b["indptr"], dtype=torch.int32))
+        kv_page_indices[:n_idx].copy_(b["indices"])
+        kv_last_page_len.copy_(torch.tensor(b["last"], dtype=torch.int32))
+        positions.copy_(torch.tensor([n - 1 for n in lens], dtype=torch.int32))
+        wrapper.plan(indptr=kv_page_indptr[:B + 1], indices=kv_page_indices[:n_idx],
+                     last_page_len=kv_last_page_len[:B], **plan_kw)
+        graph.replay()
+        torch.cuda.synchronize()
+        want_pool = opg.append(pool, k[:, :, 0], v[:, :, 0], list(range(B)), [n - 1 for n in lens],
+                               b["indices"].tolist(), b["indptr"])
+        assert torch.equal(kv_data.cpu(), want_pool), step
+        ref = oatt.decode(q[:, :, 0], want_pool, b["indptr"], b["indices"].tolist(), b["last"])
+        parity(out.float().cpu(), ref, f"step {step}")
