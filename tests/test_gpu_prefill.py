@@ -134,7 +134,8 @@ def test_head_major_q_and_out_views(dev, parity, hq, hkv, d):
     """q and out as head-major views ([heads, rows, head_dim] storage seen as
     [rows, heads, head_dim]: a head stride of rows * head_dim, larger than
     the row stride), as a single prompt's q.permute(0, 2, 1, 3).reshape(...)
-    is; every tile's rows and heads are read and written through them."""
+    is when q is a contiguous [1, heads, seq, head_dim] tensor; every tile's
+    rows and heads are read and written through them."""
     from minimal_inference_amd.prefill import BatchPrefillWithPagedKVCacheWrapper
 
     lens = [37, 300, 5, 129]
