@@ -205,6 +205,27 @@ def test_strided_q_and_out(dev, parity):
     assert torch.count_nonzero(outbuf[:, :64]) == 0
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (32, 8, 128), (28, 4, 128)])
+def test_head_major_q_and_out_views(dev, parity, hq, hkv, d):
+    """q and out as head-major views ([heads, batch, head_dim] storage seen
+    as [batch, heads, head_dim]: a head stride of batch * head_dim, larger
+    than the row stride)."""
+    lens = [40, 123, 1, 700, 16, 33]
+    b = make_paged_batch(lens, hq, hkv, d, seed=23)
+    pool, q, ip, ix, lp = to_dev(b, dev)
+    B = len(lens)
+    q_hm = q.transpose(0, 1).contiguous().transpose(0, 1)
+    out_hm = torch.full((hq, B, d), float("nan"), dtype=torch.bfloat16, device=dev).transpose(0, 1)
+    assert q_hm.stride() == (d, B * d, 1) and out_hm.stride() == q_hm.stride()
+    w = _wrapper(dev)
+    w.plan(ip, ix, lp, hq, hkv, d, 16)
+    w.run(q_hm, pool, out=out_hm)
+    torch.cuda.synchronize()
+    got = out_hm.float().cpu()
+    assert torch.isfinite(got).all()
+    parity(got, _ref(b))
+
+
 def test_graph_replay_after_replan(dev, parity):
     """run() captured once replays correctly after every later plan()."""
     hq, hkv, d = 32, 8, 128
