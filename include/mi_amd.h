@@ -188,7 +188,10 @@ int mi_decode_static(const void* q, int64_t q_stride_batch, int64_t q_stride_hea
  *   run   -- model.py:235 (mode == "prefill")
  *
  * q / out: [total_q][num_qo_heads][head_dim] bf16, rows of request b are
- * qo_indptr[b] .. qo_indptr[b+1].  With causal != 0, query row i of request b
+ * qo_indptr[b] .. qo_indptr[b+1].  Any non-negative element strides (token,
+ * head) that keep rows 16-byte aligned, including head-major views whose head
+ * stride exceeds the token stride; the positions one workgroup tile covers
+ * must span at most 2^30 elements (else MI_ERR_INVALID).  With causal != 0, query row i of request b
  * attends to KV tokens j <= i + (kv_len_b - qo_len_b) (bottom-right aligned).
  * total_q must be >= qo_indptr[batch_size]; it sizes the launch on the host.
  * plan() takes the head counts and head_dim (as FlashInfer's plan does): a
